@@ -1,0 +1,146 @@
+/*
+ * leanstack_amd.h - C ABI of the MI355X (gfx950) BF16 projection library.
+ *
+ * One shared library, libleanstack_amd.so, built with hipcc for gfx950 only.
+ * It replaces the projection arithmetic of leanstack's Qwen3 semantic runtime:
+ * the fused QKV, o_proj, fused gate_up with SiLU(gate)*up, down_proj and the
+ * tied lm_head with its argmax, at M=1 (decode), M=2..16 (speculative verify)
+ * and M in the thousands (prefill).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  Device pointers are HIP device memory
+ *     owned by the caller; the library never allocates on the compute path.
+ *   - Every compute entry point is asynchronous on `hip_stream` (a hipStream_t,
+ *     NULL = the legacy default stream) and does no host synchronisation.
+ *   - Return value: LSK_OK (0) or a negative lsk_status.  The message of the
+ *     last failure on the calling thread is returned by lsk_last_error().
+ *   - Argument checks run before anything touches the GPU, so a rejected call
+ *     launches nothing.
+ *
+ * Weight layout LSK_LAYOUT_MFMA16X32 (the packed, resident layout)
+ *   W[N][K] bf16 (N % 16 == 0, K % 32 == 0) is stored as N/16 row-blocks of
+ *   K/32 tiles of 1024 bytes each, tile (rb, kt) at byte offset
+ *   (rb * (K/32) + kt) * 1024.  Inside a tile, the 16 bytes at offset 16*l
+ *   hold W[16*rb + l%16][32*kt + 8*(l/16) + e], e = 0..7: lane l of a
+ *   64-wide wavefront loads the A operand of one v_mfma_f32_16x16x32_bf16
+ *   with one 16-byte load.
+ * Weight layout LSK_LAYOUT_MFMA16X32_GATEUP
+ *   The same tiling applied to a fused [gate; up] matrix (N = 2*I) whose
+ *   row-blocks are interleaved: packed row-block 2j holds gate rows
+ *   16j..16j+15 and packed row-block 2j+1 holds up rows 16j..16j+15, so the
+ *   SiLU(gate)*up epilogue reads both halves from the same lanes.
+ */
+#ifndef LEANSTACK_AMD_H
+#define LEANSTACK_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSK_ABI_VERSION 1
+
+enum lsk_layout {
+  LSK_LAYOUT_ROWMAJOR = 0,        /* plain W[N][K]; accepted by the packer only */
+  LSK_LAYOUT_MFMA16X32 = 1,       /* 1 KB MFMA A-operand tiles (see above) */
+  LSK_LAYOUT_MFMA16X32_GATEUP = 2 /* same tiles, gate/up row-blocks interleaved */
+};
+
+enum lsk_epilogue {
+  LSK_EPI_NONE = 0,         /* y = bf16(x . W^T) */
+  LSK_EPI_SILU_MUL = 1,     /* y = bf16(bf16(silu(bf16(g))) * bf16(u)), [g|u] = x . W^T */
+  LSK_EPI_RESIDUAL_ADD = 2  /* y = bf16(residual + bf16(x . W^T)) */
+};
+
+enum lsk_op {
+  LSK_OP_LINEAR = 0,
+  LSK_OP_LM_HEAD_ARGMAX = 1
+};
+
+enum lsk_logits_mode {
+  LSK_LOGITS_FP32 = 0,  /* argmax over fp32 scores (cuTile head semantics) */
+  LSK_LOGITS_BF16 = 1   /* argmax over bf16-rounded logits (torch.mv head semantics) */
+};
+
+enum lsk_status {
+  LSK_OK = 0,
+  LSK_ERR_INVALID = -1,    /* bad shape, stride, alignment, M or epilogue */
+  LSK_ERR_LAYOUT = -2,     /* unknown or unsupported weight layout id */
+  LSK_ERR_HIP = -3,        /* a HIP runtime call or kernel launch failed */
+  LSK_ERR_WORKSPACE = -4   /* workspace missing or smaller than lsk_workspace_bytes() */
+};
+
+/* ABI version of the loaded library (LSK_ABI_VERSION it was built with). */
+int lsk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none).  Valid until
+ * the next call into the library from the same thread. */
+const char* lsk_last_error(void);
+
+/* Bytes of one packed weight matrix W[N][K] in `layout_id`; 0 if the shape or
+ * layout is not supported.  Replaces the per-tensor size accounting of
+ * leanstack's packer (src/leanstack/pack.py:190-209). */
+size_t lsk_packed_bytes(int layout_id, int N, int K);
+
+/* Device workspace that `op` needs for M rows of an [N, K] weight.  The
+ * caller allocates it once and passes it to every call of that op.
+ * Replaces the tile_scores / tile_argmax scratch that
+ * src/leanstack/runtime/cutile_logits.py:56-58 allocates per call. */
+size_t lsk_workspace_bytes(int op, int M, int N, int K);
+
+/* Host-side packer: re-tile row-major W[N][K] bf16 (`w_rowmajor_host`) into
+ * `layout_id` at `out_host` (lsk_packed_bytes() bytes).  For
+ * LSK_LAYOUT_MFMA16X32_GATEUP the input is the fused [gate; up] matrix with
+ * gate rows first, as leanstack's packer concatenates it
+ * (src/leanstack/pack.py:281-284).  Replaces the row-major fusion of
+ * src/leanstack/pack.py:269-286. */
+int lsk_pack_bf16(const void* w_rowmajor_host, int N, int K, int layout_id, void* out_host);
+
+/* Inverse of lsk_pack_bf16 (out_rowmajor_host receives W[N][K]). */
+int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* out_rowmajor_host);
+
+/* y[M][*] = epilogue(x[M][K] . W[N][K]^T), bf16 in and out, fp32 accumulate.
+ *   w_packed   device, layout LSK_LAYOUT_MFMA16X32 (epilogue NONE / RESIDUAL_ADD)
+ *              or LSK_LAYOUT_MFMA16X32_GATEUP (epilogue SILU_MUL; N = 2*I)
+ *   x          device bf16, row m at x + m*ldx (ldx >= K, ldx % 8 == 0,
+ *              16-byte aligned)
+ *   y          device bf16, row m at y + m*ldy; N columns, or N/2 for
+ *              SILU_MUL (ldy % 4 == 0, 8-byte aligned)
+ *   residual   device bf16 [M][N] at stride ldr, RESIDUAL_ADD only (else NULL)
+ *   M          >= 1.  M <= 16 runs the decode/verify kernel (weights streamed
+ *              once, activations padded to the 16 MFMA columns); larger M
+ *              runs the prefill MFMA GEMM.
+ * Replaces torch.mv / F.linear at src/leanstack/runtime/qwen_explicit.py:748,
+ * :787, :819, :828-830, :913, :942-948, :1202-1208. */
+int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K,
+                    const void* x, int M, int ldx,
+                    void* y, int ldy,
+                    int epilogue, const void* residual, int ldr,
+                    void* workspace, size_t ws_bytes, void* hip_stream);
+
+/* Greedy lm_head: out_idx[m] = argmax_v sum_k f32(W[v][k]) * f32(x[m][k]) for
+ * m < M (M = 1..16), lowest index on ties.
+ *   logits_mode  LSK_LOGITS_FP32 compares fp32 scores, as the cuTile kernel
+ *                does (src/leanstack/runtime/cutile_logits.py:17-31, :67-69);
+ *                LSK_LOGITS_BF16 compares bf16-rounded logits, as
+ *                torch.mv(...).argmax does
+ *                (src/leanstack/runtime/qwen_explicit.py:952-960).
+ *   logits_opt   NULL, or device fp32 [M][V] that receives the scores.
+ *   out_idx      device int64 [M].
+ *   workspace    lsk_workspace_bytes(LSK_OP_LM_HEAD_ARGMAX, M, V, K) bytes.
+ * Replaces cutile_logits_argmax (src/leanstack/runtime/cutile_logits.py:37-69)
+ * and the per-position head loop of the verify path
+ * (experiments/models/qwen_explicit_runtime_loop.py:805-812) with one M-row
+ * call. */
+int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K,
+                            const void* x, int M, int ldx,
+                            float* logits_opt, int logits_mode,
+                            long long* out_idx,
+                            void* workspace, size_t ws_bytes, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LEANSTACK_AMD_H */

@@ -1,0 +1,117 @@
+"""Torch-tensor wrappers of the C ABI: projections and the greedy lm_head.
+
+Tensors are device memory that torch owns; the kernels run on torch's current
+HIP stream (``torch.cuda.current_stream().cuda_stream`` is a hipStream_t on
+ROCm), as the cuTile head launches on the current stream
+(src/leanstack/runtime/cutile_logits.py:59).  Nothing here falls back to
+another implementation: a missing library or a rejected argument raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .layout import PackedWeight
+
+
+def _require_device(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(f"{what} must be a GPU tensor, got device {t.device}")
+
+
+def _rows(x: torch.Tensor, k: int, what: str) -> tuple[torch.Tensor, int, int]:
+    """View x as [M, k] rows with unit column stride; returns (x2d, M, ld)."""
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"{what} must be bfloat16, got {x.dtype}")
+    if x.shape[-1] != k:
+        raise ValueError(f"{what} last dim {x.shape[-1]} != K={k}")
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) % 8) or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    ld = x2.stride(0) if x2.shape[0] > 1 else k
+    return x2, x2.shape[0], ld
+
+
+def stream_handle() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NONE,
+           residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[..., N'] = epilogue(x[..., K] . W^T) on the GPU.
+
+    epilogue EPI_NONE (N' = N), EPI_SILU_MUL (gate_up layout, N' = N/2,
+    SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection)."""
+    if not isinstance(weight, PackedWeight):
+        raise ValueError("weight must be a PackedWeight (pack it with leanstack_amd.layout / leanserve)")
+    lib = _lib.load()
+    _require_device(x, "x")
+    _require_device(weight.data, "weight")
+    x2, m, ldx = _rows(x, weight.k, "x")
+    n_out = weight.n // 2 if epilogue == _lib.EPI_SILU_MUL else weight.n
+    lead = x.shape[:-1]
+    if out is None:
+        out = torch.empty((*lead, n_out), device=x.device, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bfloat16 [..., {n_out}] tensor")
+    res_ptr, ldr = None, 0
+    if residual is not None:
+        _require_device(residual, "residual")
+        r2, rm, ldr = _rows(residual, weight.n, "residual")
+        if rm != m:
+            raise ValueError(f"residual has {rm} rows, x has {m}")
+        res_ptr = r2.data_ptr()
+    status = lib.lsk_linear_bf16(
+        weight.data.data_ptr(), weight.layout, weight.n, weight.k,
+        x2.data_ptr(), m, ldx,
+        out.data_ptr(), n_out,
+        epilogue, res_ptr, ldr,
+        None, 0, stream_handle(),
+    )
+    _lib.check(status, "lsk_linear_bf16")
+    return out
+
+
+class LmHeadWorkspace:
+    """Device workspace of the two-stage argmax, sized once per (M, V, K)."""
+
+    def __init__(self, m: int, v: int, k: int, device: torch.device | str) -> None:
+        nbytes = _lib.load().lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, m, v, k)
+        if nbytes == 0:
+            raise ValueError(f"no lm_head workspace for M={m}, V={v}, K={k}")
+        self.m, self.v, self.k = m, v, k
+        self.buffer = torch.empty(nbytes, device=device, dtype=torch.uint8)
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: int = _lib.LOGITS_FP32,
+                   logits_out: torch.Tensor | None = None, workspace: LmHeadWorkspace | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Greedy token per row: int64 [M] = argmax over the vocab of hidden . W^T.
+
+    logits_mode LOGITS_FP32 compares fp32 scores (cuTile head); LOGITS_BF16
+    compares bf16-rounded logits (torch.mv head).  Lowest index wins ties."""
+    if not isinstance(weight, PackedWeight) or weight.layout != _lib.LAYOUT_MFMA16X32:
+        raise ValueError("lm_head weight must be a PackedWeight in the mfma16x32 layout")
+    lib = _lib.load()
+    _require_device(hidden, "hidden")
+    h2, m, ldx = _rows(hidden, weight.k, "hidden")
+    v = weight.n
+    if workspace is None or workspace.m < m or workspace.v != v or workspace.k != weight.k:
+        workspace = LmHeadWorkspace(m, v, weight.k, hidden.device)
+    if out is None:
+        out = torch.empty((m,), device=hidden.device, dtype=torch.long)
+    logits_ptr = None
+    if logits_out is not None:
+        if logits_out.dtype != torch.float32 or logits_out.numel() != m * v or not logits_out.is_contiguous():
+            raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{v}")
+        logits_ptr = logits_out.data_ptr()
+    status = lib.lsk_lm_head_argmax_bf16(
+        weight.data.data_ptr(), weight.layout, v, weight.k,
+        h2.data_ptr(), m, ldx,
+        logits_ptr, logits_mode,
+        out.data_ptr(),
+        workspace.buffer.data_ptr(), workspace.buffer.numel(), stream_handle(),
+    )
+    _lib.check(status, "lsk_lm_head_argmax_bf16")
+    return out

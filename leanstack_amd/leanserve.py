@@ -1,0 +1,280 @@
+"""leanserve for the MI355X path: a resident arena planner that allocates.
+
+The reference's planner is descriptive only: it sums file sizes, sizes the KV
+cache per bucket and estimates scratch with bf16 logits, and never allocates
+(src/leanstack/leanserve.py:331-377).  Here the plan is the allocation: one
+device buffer (one hipMalloc through torch) holds every packed projection
+weight of all layers, the norms, the row-major embedding, a packed copy of
+the tied lm_head, the activation scratch for the largest row count a call
+may carry, fp32 logits, the argmax workspace and the KV cache of the largest
+bucket.  Every entry is a fixed, aligned view; nothing is allocated after
+start-up.  With 288 GB of HBM the whole Qwen3-4B stack (about 8.8 GB) is
+resident with room to spare.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from math import ceil
+from typing import Iterable
+
+import torch
+
+from . import _lib
+from .geometry import QWEN3_4B, QwenGeometry
+from .layout import PackedWeight
+
+ARENA_ALIGNMENT = 4096
+
+_DTYPE_BYTES = {torch.bfloat16: 2, torch.float32: 4, torch.int64: 8, torch.uint8: 1}
+_DTYPE_NAMES = {torch.bfloat16: "bfloat16", torch.float32: "float32", torch.int64: "int64", torch.uint8: "uint8"}
+
+
+@dataclass(frozen=True)
+class ArenaEntry:
+    name: str
+    role: str
+    offset: int
+    nbytes: int
+    dtype: str
+    shape: tuple[int, ...]
+    layout: int | None = None  # packed layout id for projection weights
+
+    @property
+    def end(self) -> int:
+        return self.offset + self.nbytes
+
+
+@dataclass(frozen=True)
+class ScratchPlan:
+    """Activation scratch for `rows` rows (the reference sizes one row and bf16
+    logits, src/leanstack/leanserve.py:341-347; here logits are fp32, the
+    precision the greedy head compares in)."""
+
+    rows: int
+    hidden_state_bytes: int
+    residual_bytes: int
+    qkv_projection_bytes: int
+    attention_output_bytes: int
+    mlp_activation_bytes: int
+    logits_bytes: int
+    argmax_workspace_bytes: int
+    token_bytes: int
+
+    @property
+    def total_bytes(self) -> int:
+        return (
+            self.hidden_state_bytes + self.residual_bytes + self.qkv_projection_bytes
+            + self.attention_output_bytes + self.mlp_activation_bytes + self.logits_bytes
+            + self.argmax_workspace_bytes + self.token_bytes
+        )
+
+
+@dataclass(frozen=True)
+class BucketSpec:
+    key: str
+    prompt_tokens: int
+    max_new_tokens: int
+
+
+@dataclass(frozen=True)
+class ResidentBucketPlan:
+    key: str
+    prompt_tokens: int
+    max_new_tokens: int
+    max_seq_len: int
+    kv_tokens_capacity: int
+    kv_cache_bytes: int
+
+
+@dataclass(frozen=True)
+class ResidentBufferPlan:
+    geometry: QwenGeometry
+    layers: int
+    weights_bytes: int
+    page_size: int
+    batch_size: int
+    scratch: ScratchPlan
+    buckets: tuple[ResidentBucketPlan, ...]
+    entries: tuple[ArenaEntry, ...] = field(default_factory=tuple)
+    alignment: int = ARENA_ALIGNMENT
+
+    @property
+    def max_kv_cache_bytes(self) -> int:
+        return max((b.kv_cache_bytes for b in self.buckets), default=0)
+
+    @property
+    def resident_bytes(self) -> int:
+        """Payload bytes (before alignment padding), as the reference reports."""
+        return self.weights_bytes + self.max_kv_cache_bytes + self.scratch.total_bytes
+
+    @property
+    def arena_bytes(self) -> int:
+        return max((e.end for e in self.entries), default=0)
+
+    def entry(self, name: str) -> ArenaEntry:
+        for e in self.entries:
+            if e.name == name:
+                return e
+        raise KeyError(name)
+
+
+# The reference's benchmark buckets (src/leanstack/benchmark.py:59-93).
+DEFAULT_BUCKETS = (
+    BucketSpec("decode_64_256", 64, 256),
+    BucketSpec("decode_64_512", 64, 512),
+    BucketSpec("prefill_1024_64", 1024, 64),
+)
+
+
+class _Planner:
+    def __init__(self, alignment: int) -> None:
+        self.alignment = alignment
+        self.offset = 0
+        self.entries: list[ArenaEntry] = []
+
+    def add(self, name: str, role: str, dtype: torch.dtype, shape: tuple[int, ...], layout: int | None = None) -> None:
+        nbytes = _DTYPE_BYTES[dtype]
+        for d in shape:
+            nbytes *= d
+        self.offset = ceil(self.offset / self.alignment) * self.alignment
+        self.entries.append(ArenaEntry(name, role, self.offset, nbytes, _DTYPE_NAMES[dtype], tuple(shape), layout))
+        self.offset += nbytes
+
+
+def layer_entry_names(layer: int) -> dict[str, str]:
+    p = f"layers.{layer}."
+    return {
+        "input_layernorm": p + "input_layernorm.weight",
+        "qkv_proj": p + "attention.qkv_proj.weight",
+        "o_proj": p + "attention.o_proj.weight",
+        "q_norm": p + "attention.q_norm.weight",
+        "k_norm": p + "attention.k_norm.weight",
+        "post_attention_layernorm": p + "post_attention_layernorm.weight",
+        "gate_up_proj": p + "mlp.gate_up_proj.weight",
+        "down_proj": p + "mlp.down_proj.weight",
+    }
+
+
+def build_resident_buffer_plan(
+    geometry: QwenGeometry = QWEN3_4B,
+    *,
+    layers: int | None = None,
+    buckets: Iterable[BucketSpec] = DEFAULT_BUCKETS,
+    page_size: int = 16,
+    batch_size: int = 1,
+    max_rows: int = 16,
+    include_embedding: bool = True,
+    include_lm_head: bool = True,
+    alignment: int = ARENA_ALIGNMENT,
+) -> ResidentBufferPlan:
+    """Lay out every resident tensor in one arena (offsets aligned to `alignment`).
+
+    `max_rows` is the largest M any projection call carries (16 covers decode
+    and speculative verify; a prefill bucket raises it to the prompt length)."""
+    g = geometry
+    n_layers = g.num_hidden_layers if layers is None else layers
+    pl = _Planner(alignment)
+    bf16 = torch.bfloat16
+    weights = 0
+    if include_embedding:
+        pl.add("model.embed_tokens.weight", "embedding", bf16, (g.vocab_size, g.hidden_size))
+    for layer in range(n_layers):
+        names = layer_entry_names(layer)
+        proj = g.projections()
+        pl.add(names["input_layernorm"], "input_layernorm", bf16, (g.hidden_size,))
+        pl.add(names["qkv_proj"], "attention_qkv_fused", bf16, proj["qkv_proj"], _lib.LAYOUT_MFMA16X32)
+        pl.add(names["o_proj"], "attention_output_projection", bf16, proj["o_proj"], _lib.LAYOUT_MFMA16X32)
+        pl.add(names["q_norm"], "attention_q_norm", bf16, (g.head_dim,))
+        pl.add(names["k_norm"], "attention_k_norm", bf16, (g.head_dim,))
+        pl.add(names["post_attention_layernorm"], "post_attention_layernorm", bf16, (g.hidden_size,))
+        pl.add(names["gate_up_proj"], "mlp_gate_up_fused", bf16, proj["gate_up_proj"], _lib.LAYOUT_MFMA16X32_GATEUP)
+        pl.add(names["down_proj"], "mlp_down_projection", bf16, proj["down_proj"], _lib.LAYOUT_MFMA16X32)
+    pl.add("model.norm.weight", "final_norm", bf16, (g.hidden_size,))
+    if include_lm_head:
+        pl.add("lm_head.weight", "lm_head", bf16, (g.vocab_size, g.hidden_size), _lib.LAYOUT_MFMA16X32)
+    weights = sum(e.nbytes for e in pl.entries)
+
+    head_rows = min(max_rows, 16)
+    lib = _lib.load()
+    ws = lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, head_rows, g.vocab_size, g.hidden_size) if include_lm_head else 0
+    scratch = ScratchPlan(
+        rows=max_rows,
+        hidden_state_bytes=max_rows * g.hidden_size * 2,
+        residual_bytes=max_rows * g.hidden_size * 2,
+        qkv_projection_bytes=max_rows * g.qkv_dim * 2,
+        attention_output_bytes=max_rows * g.q_dim * 2,
+        mlp_activation_bytes=max_rows * g.intermediate_size * 2,
+        logits_bytes=head_rows * g.vocab_size * 4 if include_lm_head else 0,
+        argmax_workspace_bytes=ws,
+        token_bytes=head_rows * 8,
+    )
+    pl.add("scratch.hidden", "scratch", bf16, (max_rows, g.hidden_size))
+    pl.add("scratch.residual", "scratch", bf16, (max_rows, g.hidden_size))
+    pl.add("scratch.qkv", "scratch", bf16, (max_rows, g.qkv_dim))
+    pl.add("scratch.attn", "scratch", bf16, (max_rows, g.q_dim))
+    pl.add("scratch.mlp_act", "scratch", bf16, (max_rows, g.intermediate_size))
+    if include_lm_head:
+        pl.add("scratch.logits", "scratch", torch.float32, (head_rows, g.vocab_size))
+        pl.add("scratch.argmax_workspace", "scratch", torch.uint8, (ws,))
+    pl.add("scratch.tokens", "scratch", torch.int64, (head_rows,))
+
+    bucket_plans = []
+    for b in buckets:
+        max_seq = int(b.prompt_tokens) + int(b.max_new_tokens)
+        cap = ceil(max_seq / page_size) * page_size
+        kv = batch_size * n_layers * 2 * g.num_key_value_heads * g.head_dim * cap * 2
+        bucket_plans.append(ResidentBucketPlan(b.key, b.prompt_tokens, b.max_new_tokens, max_seq, cap, kv))
+    if bucket_plans:
+        cap = max(b.kv_tokens_capacity for b in bucket_plans)
+        pl.add("kv_cache", "kv_cache", bf16, (n_layers, 2, batch_size, g.num_key_value_heads, cap, g.head_dim))
+
+    return ResidentBufferPlan(
+        geometry=g, layers=n_layers, weights_bytes=weights, page_size=page_size, batch_size=batch_size,
+        scratch=scratch, buckets=tuple(bucket_plans), entries=tuple(pl.entries), alignment=alignment,
+    )
+
+
+_TORCH_DTYPES = {v: k for k, v in _DTYPE_NAMES.items()}
+
+
+class ResidentArena:
+    """The allocation behind a ResidentBufferPlan: one device buffer, typed views."""
+
+    def __init__(self, plan: ResidentBufferPlan, device: torch.device | str) -> None:
+        self.plan = plan
+        self.device = torch.device(device)
+        self.buffer = torch.empty(plan.arena_bytes, dtype=torch.uint8, device=self.device)
+        if self.buffer.data_ptr() % 256:
+            raise RuntimeError("arena base is not 256-byte aligned")
+        self._index = {e.name: e for e in plan.entries}
+
+    def view(self, name: str) -> torch.Tensor:
+        e = self._index[name]
+        raw = self.buffer[e.offset : e.end]
+        return raw.view(_TORCH_DTYPES[e.dtype]).view(e.shape)
+
+    def packed(self, name: str) -> PackedWeight:
+        e = self._index[name]
+        if e.layout is None:
+            raise ValueError(f"{name} is not a packed projection weight")
+        flat = self.buffer[e.offset : e.end].view(torch.bfloat16)
+        n, k = e.shape
+        return PackedWeight(flat, n, k, e.layout)
+
+    def store_rowmajor(self, name: str, w: torch.Tensor) -> None:
+        """Copy a row-major weight into its entry, packing projection weights."""
+        e = self._index[name]
+        if tuple(w.shape) != e.shape:
+            raise ValueError(f"{name}: shape {tuple(w.shape)} != planned {e.shape}")
+        if e.layout is None:
+            self.view(name).copy_(w)
+        else:
+            PackedWeight.from_rowmajor(w.to(self.device, torch.bfloat16), e.layout,
+                                       out=self.buffer[e.offset : e.end].view(torch.bfloat16))
+
+    def store_packed(self, name: str, packed: torch.Tensor) -> None:
+        e = self._index[name]
+        if e.layout is None or packed.numel() * 2 != e.nbytes:
+            raise ValueError(f"{name}: not a packed entry of {e.nbytes} bytes")
+        self.buffer[e.offset : e.end].view(torch.bfloat16).copy_(packed.reshape(-1))

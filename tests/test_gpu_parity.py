@@ -1,0 +1,193 @@
+"""GPU parity of the HIP projections against the CPU oracle (same seeded inputs).
+
+Bar: cosine >= 0.9999 and normwise max relative error <= 1e-2 for bf16
+outputs with fp32 accumulation; exact argmax for the lm_head.  Every case
+calls the C ABI through leanstack_amd.kernels.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from leanstack_amd import _lib, kernels
+from leanstack_amd.geometry import QWEN3_4B as G
+from leanstack_amd.layout import PackedWeight
+from oracle import brute
+from oracle import projections as ref
+from tests.helpers import activations, assert_parity, bits, weight
+
+pytestmark = pytest.mark.gpu
+
+PROJ = {
+    "qkv_proj": (G.qkv_dim, G.hidden_size),
+    "o_proj": (G.hidden_size, G.q_dim),
+    "down_proj": (G.hidden_size, G.intermediate_size),
+}
+
+
+def _gpu_linear(x, w, layout=_lib.LAYOUT_MFMA16X32, epilogue=_lib.EPI_NONE, residual=None):
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(w.to(dev), layout)
+    res = residual.to(dev) if residual is not None else None
+    y = kernels.linear(x.to(dev), pw, epilogue=epilogue, residual=res)
+    torch.cuda.synchronize()
+    return y.cpu()
+
+
+def test_o_proj_gemv_config1(gpu):
+    """x[1,4096] ~ N(0,1), W[2560,4096] ~ N(0,0.02): elementwise within bf16
+    rounding + the fp32 summation bound of the float64 brute force."""
+    w = weight(2560, 4096, seed=0)
+    x = activations(1, 4096, seed=1)
+    y = _gpu_linear(x, w)
+    assert_parity(y.view(-1), ref.mv(w, x.view(-1)), "o_proj M=1 vs torch.mv")
+    y64 = brute.linear64(bits(x), bits(w))
+    bound = brute.fp32_sum_bound(bits(x), bits(w))
+    got = y.double().numpy()
+    slack = 0.5 * np.maximum(brute.bf16_ulp(y64), brute.bf16_ulp(got)) + bound
+    assert np.all(np.abs(got - y64) <= slack)
+
+
+@pytest.mark.parametrize("name", sorted(PROJ))
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+def test_decode_projection(gpu, name, m):
+    n, k = PROJ[name]
+    w = weight(n, k, seed=10 + m)
+    x = activations(m, k, seed=100 + m)
+    y = _gpu_linear(x, w)
+    expect = ref.mv(w, x.view(-1)).view(1, -1) if m == 1 else ref.linear(x, w)
+    assert_parity(y, expect, f"{name} M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_decode_gate_up_silu(gpu, m):
+    n, k = 2 * G.intermediate_size, G.hidden_size
+    w = weight(n, k, seed=20 + m)
+    x = activations(m, k, seed=200 + m)
+    y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
+    expect = ref.silu_mul(ref.linear(x, w), G.intermediate_size)
+    assert_parity(y, expect, f"gate_up+silu M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_decode_down_residual(gpu, m):
+    n, k = G.hidden_size, G.intermediate_size
+    w = weight(n, k, seed=30 + m)
+    x = activations(m, k, seed=300 + m)
+    r = activations(m, n, seed=301 + m)
+    y = _gpu_linear(x, w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r)
+    assert_parity(y, r + ref.linear(x, w), f"down+residual M={m}")
+
+
+@pytest.mark.parametrize("name", sorted(PROJ))
+@pytest.mark.parametrize("m", [17, 128, 300])
+def test_prefill_projection(gpu, name, m):
+    n, k = PROJ[name]
+    w = weight(n, k, seed=40 + m)
+    x = activations(m, k, seed=400 + m)
+    y = _gpu_linear(x, w)
+    assert_parity(y, ref.linear(x, w), f"{name} prefill M={m}")
+
+
+@pytest.mark.parametrize("m", [64, 257])
+def test_prefill_gate_up_silu(gpu, m):
+    n, k = 2 * G.intermediate_size, G.hidden_size
+    w = weight(n, k, seed=50 + m)
+    x = activations(m, k, seed=500 + m)
+    y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
+    expect = ref.silu_mul(ref.linear(x, w), G.intermediate_size)
+    assert_parity(y, expect, f"gate_up+silu prefill M={m}")
+
+
+def test_prefill_residual(gpu):
+    m, n, k = 200, G.hidden_size, G.q_dim
+    w = weight(n, k, seed=60)
+    x = activations(m, k, seed=600)
+    r = activations(m, n, seed=601)
+    y = _gpu_linear(x, w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r)
+    assert_parity(y, r + ref.linear(x, w), "o_proj+residual prefill")
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_lm_head_argmax_fp32(gpu, m):
+    """Tied lm_head E[151936, 2560]: GPU argmax == CPU fp32-score argmax."""
+    e = weight(G.vocab_size, G.hidden_size, seed=70)
+    h = activations(m, G.hidden_size, seed=700 + m)
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(e.to(dev))
+    logits = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
+    idx = kernels.lm_head_argmax(h.to(dev), pw, logits_out=logits).cpu()
+    scores = ref.logits_scores_fp32(h, e)
+    expect = scores.argmax(dim=-1)
+    margin = ref.top2_margin(scores)
+    print(f"M={m} idx={idx.tolist()} margin={margin.tolist()}")
+    assert torch.equal(idx, expect)
+    assert_parity(logits.cpu(), scores, "lm_head fp32 logits")
+
+
+def test_lm_head_argmax_bf16_mode(gpu):
+    """bf16-rounded logits: matches torch.mv(W, h).argmax (first maximum)."""
+    e = weight(G.vocab_size, G.hidden_size, seed=71)
+    h = activations(1, G.hidden_size, seed=710)
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(e.to(dev))
+    logits = torch.empty((1, G.vocab_size), device=dev, dtype=torch.float32)
+    idx = kernels.lm_head_argmax(h.to(dev), pw, logits_mode=_lib.LOGITS_BF16, logits_out=logits).cpu()
+    expect = ref.bf16_logits_argmax(h, e)
+    bf = torch.mv(e, h.view(-1)).float()
+    top = torch.topk(bf, 2).values
+    print(f"idx={idx.tolist()} expect={expect.tolist()} top2={top.tolist()}")
+    assert torch.equal(idx, expect)
+
+
+def test_lm_head_ties_pick_lowest_index(gpu):
+    """Two identical maximal vocab rows: the lower index wins, in both modes."""
+    v, k = 4096, 256
+    e = weight(v, k, seed=72)
+    h = activations(1, k, seed=720)
+    hot = torch.sign(h.float()).to(torch.bfloat16) * 0.5
+    e[1234] = hot
+    e[3001] = hot
+    e[17] = -hot
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(e.to(dev))
+    for mode in (_lib.LOGITS_FP32, _lib.LOGITS_BF16):
+        idx = kernels.lm_head_argmax(h.to(dev), pw, logits_mode=mode).cpu()
+        assert idx.tolist() == [1234]
+
+
+def test_device_pack_matches_host_packer(gpu):
+    """torch-permute packing on the GPU equals the C host packer, byte for byte."""
+    w = weight(2 * 256, 512, seed=80)
+    lib = _lib.load()
+    for layout in (_lib.LAYOUT_MFMA16X32, _lib.LAYOUT_MFMA16X32_GATEUP):
+        dev_packed = PackedWeight.from_rowmajor(w.to("cuda:0"), layout).data.cpu()
+        host = torch.empty_like(w).view(-1)
+        status = lib.lsk_pack_bf16(w.data_ptr(), w.shape[0], w.shape[1], layout, host.data_ptr())
+        _lib.check(status, "pack")
+        assert torch.equal(dev_packed.view(torch.int16), host.view(torch.int16))
+
+
+def test_strided_activations(gpu):
+    """x rows at a stride larger than K (a column slice of a wider buffer)."""
+    n, k, m = 2560, 4096, 4
+    w = weight(n, k, seed=90)
+    wide = activations(m, k + 64, seed=900)
+    x = wide[:, 32 : 32 + k]
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(w.to(dev))
+    y = kernels.linear(wide.to(dev)[:, 32 : 32 + k], pw).cpu()
+    assert_parity(y, ref.linear(x, w), "strided x")
+
+
+def test_rejects_bad_shapes_before_launch(gpu):
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(weight(64, 64, seed=1).to(dev))
+    with pytest.raises(ValueError):
+        kernels.linear(activations(1, 32, seed=2).to(dev), pw)
+    with pytest.raises(ValueError):
+        kernels.linear(activations(1, 64, seed=2).to(dev), pw, epilogue=_lib.EPI_SILU_MUL)
+    with pytest.raises(ValueError):
+        kernels.lm_head_argmax(activations(17, 64, seed=2).to(dev), pw)
