@@ -139,6 +139,59 @@ int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K,
                             long long* out_idx,
                             void* workspace, size_t ws_bytes, void* hip_stream);
 
+/* ------------------------------------------------------------------------
+ * Stack programs: a whole decode / verify step of projections in ONE launch.
+ *
+ * A program is a list of projections with the semantics of lsk_linear_bf16
+ * (all at the same M = 1..16 rows) plus a dependency per projection.  The
+ * persistent kernel streams the weights of every projection in order and
+ * starts loading a projection's weights before its input is ready; only the
+ * multiply waits.  This replaces the per-layer Python loop of
+ * run_semantic_stack_decode (src/leanstack/runtime/qwen_explicit.py:1636-1643)
+ * and its 4 projection launches per layer.
+ * ------------------------------------------------------------------------ */
+
+typedef struct lsk_projection {
+  const void* w_packed;  /* packed weights, as for lsk_linear_bf16 */
+  int layout_id;
+  int N;
+  int K;                 /* K/32 must be a multiple of 8 and >= 8 */
+  const void* x;         /* input rows [M][K] at stride ldx */
+  int ldx;
+  void* y;               /* output rows at stride ldy */
+  int ldy;
+  int epilogue;          /* lsk_epilogue */
+  const void* residual;  /* RESIDUAL_ADD only, else NULL */
+  int ldr;
+  int depends_on;        /* -1: inputs ready at launch; q (< this index):
+                            every projection 0..q finishes before this one
+                            reads x or residual */
+} lsk_projection;
+
+/* Device bytes of a program of `count` projections. */
+size_t lsk_stack_program_bytes(int count);
+
+/* Device workspace bytes of a program of `count` projections.  The caller
+ * zeroes it once before the first launch; every launch leaves it zeroed
+ * (except the error word, see lsk_stack_error). */
+size_t lsk_stack_workspace_bytes(int count);
+
+/* Validate `projections` (host array) and upload the program to program_dev
+ * (device, lsk_stack_program_bytes(count) bytes).  Synchronous; set-up only. */
+int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void* program_dev,
+                      size_t program_bytes);
+
+/* Launch a prepared program on hip_stream (one kernel; capturable in a HIP
+ * graph).  No other kernel may run on the device concurrently: the program
+ * keeps one workgroup resident per CU.  Launches that share a workspace must
+ * be stream-ordered. */
+int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws_bytes, void* hip_stream);
+
+/* Read (synchronously) and clear the workspace's error word: 0 = every wait
+ * of every launch since the last call completed; nonzero = a bounded wait
+ * gave up (outputs of that launch are invalid). */
+int lsk_stack_error(void* workspace, int* error_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,33 @@ _SIGNATURES: dict[str, tuple[type | None, list]] = {
     ),
 }
 
+class Projection(ctypes.Structure):
+    """struct lsk_projection (include/leanstack_amd.h)."""
+
+    _fields_ = [
+        ("w_packed", _c_void),
+        ("layout_id", _c_int),
+        ("N", _c_int),
+        ("K", _c_int),
+        ("x", _c_void),
+        ("ldx", _c_int),
+        ("y", _c_void),
+        ("ldy", _c_int),
+        ("epilogue", _c_int),
+        ("residual", _c_void),
+        ("ldr", _c_int),
+        ("depends_on", _c_int),
+    ]
+
+
+_SIGNATURES.update({
+    "lsk_stack_program_bytes": (_c_size, [_c_int]),
+    "lsk_stack_workspace_bytes": (_c_size, [_c_int]),
+    "lsk_stack_prepare": (_c_int, [ctypes.POINTER(Projection), _c_int, _c_int, _c_void, _c_size]),
+    "lsk_stack_run": (_c_int, [_c_void, _c_int, _c_void, _c_size, _c_void]),
+    "lsk_stack_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
+})
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 

@@ -14,7 +14,9 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "lsk_internal.h"
 
@@ -198,6 +200,140 @@ int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, c
                                               out_idx, static_cast<lsk::ArgmaxPartial*>(workspace),
                                               static_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess) return hip_fail(err, "lm_head kernel launch");
+  return LSK_OK;
+}
+
+}  // extern "C"
+
+// ----------------------------------------------------------------- stack programs
+
+namespace {
+
+// Persistent grid size per device: CUs x resident workgroups per CU.
+int stack_grid(int device, size_t lds_bytes, int* grid_out) {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  if (device >= (int)cache.size()) cache.resize(device + 1, 0);
+  if (cache[device] == 0) {
+    int cus = 0;
+    hipError_t err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute(multiprocessor count)");
+    int per_cu = 0;
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, lsk::stack_kernel_symbol(), lsk::kStackWaves * 64,
+                                                       lds_bytes);
+    if (err != hipSuccess) return hip_fail(err, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (cus <= 0 || per_cu <= 0) return fail(LSK_ERR_HIP, "stack kernel cannot be resident (cus=%d, per_cu=%d)", cus, per_cu);
+    cache[device] = cus * per_cu;
+  }
+  *grid_out = cache[device];
+  return LSK_OK;
+}
+
+size_t stack_program_bytes(int count) {
+  return sizeof(lsk::StackProgram) + (size_t)(count > 1 ? count - 1 : 0) * sizeof(lsk::StackDesc);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t lsk_stack_program_bytes(int count) { return count > 0 ? stack_program_bytes(count) : 0; }
+
+size_t lsk_stack_workspace_bytes(int count) {
+  if (count <= 0) return 0;
+  const size_t words = (size_t)lsk::kStackWsCounters + (size_t)count;
+  return (words * sizeof(unsigned) + 255) / 256 * 256;
+}
+
+int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void* program_dev, size_t program_bytes) {
+  g_last_error.clear();
+  if (projections == nullptr || count <= 0) return fail(LSK_ERR_INVALID, "empty stack program");
+  if (M < 1 || M > lsk::kDecodeMaxM) return fail(LSK_ERR_INVALID, "stack M=%d must be in 1..%d", M, lsk::kDecodeMaxM);
+  if (program_dev == nullptr || program_bytes < stack_program_bytes(count) || !aligned(program_dev, 64))
+    return fail(LSK_ERR_INVALID, "program buffer needs %zu bytes, 64-byte aligned", stack_program_bytes(count));
+  std::vector<unsigned char> host(stack_program_bytes(count), 0);
+  auto* prog = reinterpret_cast<lsk::StackProgram*>(host.data());
+  prog->count = count;
+  prog->M = M;
+  prog->magic = lsk::kStackMagic;
+  int item_begin = 0;
+  for (int i = 0; i < count; ++i) {
+    const lsk_projection& p = projections[i];
+    if (int st = check_shape(p.layout_id, p.N, p.K)) return fail(st, "projection %d: %s", i, g_last_error.c_str());
+    const int KT = p.K / lsk::kTileK;
+    if (KT % lsk::kStackWaves != 0)
+      return fail(LSK_ERR_INVALID, "projection %d: K/32=%d must be a multiple of %d", i, KT, lsk::kStackWaves);
+    if (p.epilogue != LSK_EPI_NONE && p.epilogue != LSK_EPI_SILU_MUL && p.epilogue != LSK_EPI_RESIDUAL_ADD)
+      return fail(LSK_ERR_INVALID, "projection %d: unknown epilogue %d", i, p.epilogue);
+    if ((p.epilogue == LSK_EPI_SILU_MUL) != (p.layout_id == LSK_LAYOUT_MFMA16X32_GATEUP))
+      return fail(LSK_ERR_INVALID, "projection %d: SiLU*up needs the interleaved gate_up layout and vice versa", i);
+    if (p.w_packed == nullptr || p.x == nullptr || p.y == nullptr || !aligned(p.w_packed, 16))
+      return fail(LSK_ERR_INVALID, "projection %d: null or misaligned pointer", i);
+    if (p.ldx < p.K || p.ldx % 8 != 0 || !aligned(p.x, 16))
+      return fail(LSK_ERR_INVALID, "projection %d: x needs ldx >= K, ldx %% 8 == 0, 16-byte alignment", i);
+    const int n_out = p.epilogue == LSK_EPI_SILU_MUL ? p.N / 2 : p.N;
+    if (p.ldy < n_out || p.ldy % 4 != 0 || !aligned(p.y, 8))
+      return fail(LSK_ERR_INVALID, "projection %d: y needs ldy >= %d, ldy %% 4 == 0, 8-byte alignment", i, n_out);
+    if (p.epilogue == LSK_EPI_RESIDUAL_ADD) {
+      if (p.residual == nullptr || p.ldr < p.N || p.ldr % 4 != 0 || !aligned(p.residual, 8))
+        return fail(LSK_ERR_INVALID, "projection %d: residual [M][N] needs ldr >= N, ldr %% 4 == 0, 8-byte alignment",
+                    i);
+    } else if (p.residual != nullptr) {
+      return fail(LSK_ERR_INVALID, "projection %d: residual without the residual-add epilogue", i);
+    }
+    if (p.depends_on < -1 || p.depends_on >= i)
+      return fail(LSK_ERR_INVALID, "projection %d: depends_on=%d must be -1 or an earlier index", i, p.depends_on);
+    lsk::StackDesc& d = prog->desc[i];
+    d.w = static_cast<const lsk::bf16x8_t*>(p.w_packed);
+    d.x = static_cast<const __bf16*>(p.x);
+    d.y = static_cast<__bf16*>(p.y);
+    d.res = static_cast<const __bf16*>(p.residual);
+    d.KT = KT;
+    d.ldx = p.ldx;
+    d.ldy = p.ldy;
+    d.ldr = p.ldr;
+    d.epi = p.epilogue;
+    d.rbw = p.epilogue == LSK_EPI_SILU_MUL ? 2 : 1;
+    d.items = p.N / lsk::kTileRows / d.rbw;
+    d.item_begin = item_begin;
+    d.dep = p.depends_on;
+    item_begin += d.items;
+  }
+  prog->total_items = item_begin;
+  hipError_t err = hipMemcpy(program_dev, host.data(), host.size(), hipMemcpyHostToDevice);
+  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(stack program)");
+  return LSK_OK;
+}
+
+int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws_bytes, void* hip_stream) {
+  g_last_error.clear();
+  if (program_dev == nullptr || count <= 0) return fail(LSK_ERR_INVALID, "null or empty stack program");
+  if (workspace == nullptr || ws_bytes < lsk_stack_workspace_bytes(count) || !aligned(workspace, 256))
+    return fail(LSK_ERR_WORKSPACE, "stack workspace needs %zu bytes, 256-byte aligned", lsk_stack_workspace_bytes(count));
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+  const size_t lds = lsk::stack_lds_bytes();
+  int grid = 0;
+  if (int st = stack_grid(device, lds, &grid)) return st;
+  err = lsk::launch_decode_stack(static_cast<const lsk::StackProgram*>(program_dev), static_cast<unsigned*>(workspace),
+                                 grid, lds, static_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess) return hip_fail(err, "stack kernel launch");
+  return LSK_OK;
+}
+
+int lsk_stack_error(void* workspace, int* error_out) {
+  g_last_error.clear();
+  if (workspace == nullptr || error_out == nullptr) return fail(LSK_ERR_INVALID, "null argument");
+  unsigned word = 0;
+  auto* err_word = static_cast<unsigned*>(workspace) + lsk::kStackWsError;
+  hipError_t err = hipMemcpy(&word, err_word, sizeof(word), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(stack error word)");
+  const unsigned zero = 0;
+  err = hipMemcpy(err_word, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(clear stack error word)");
+  *error_out = (int)word;
   return LSK_OK;
 }
 

@@ -28,7 +28,6 @@
 namespace lsk {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
@@ -74,31 +73,56 @@ __device__ __forceinline__ float silu_mul_bf16(float g_acc, float u_acc) {
 // Accumulate RBW row-blocks over this wave's K range into acc.
 //   wt   : tile (rb0, 0) of the workgroup, already offset by `lane`
 //   xrow : x row (m, or row 0 for padding lanes), as 16-byte units, + g
+// U > 0: the range is exactly U k-tiles and every weight load of the wave is
+// issued in one round (one memory latency per wave).  U == 0: any length,
+// in rounds of 8 / RBW k-tiles plus a remainder.
 template <int RBW, int U>
 __device__ __forceinline__ void accumulate_rows(f32x4_t (&acc)[RBW], const bf16x8_t* __restrict__ wt,
                                                 const bf16x8_t* __restrict__ xrow, bool m_active,
                                                 int KT, int kb, int ke) {
   const unsigned keep = m_active ? 0xffffffffu : 0u;
-  int kt = kb;
-  for (; kt + U <= ke; kt += U) {
-    bf16x8_t xv[U];
+  if constexpr (U > 0) {
+    // One round: every weight load of the wave goes out first (the HBM
+    // latency is paid once), then the activation fragments -- L2 hits --
+    // are fetched next to the multiplies that use them, which keeps the
+    // register footprint at the weights plus a short window.
     bf16x8_t wv[U][RBW];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      xv[u] = load_x_frag(xrow + (kt + u) * 4, keep);
 #pragma unroll
-      for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kt + u) * 64);
+      for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kb + u) * 64);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      const bf16x8_t xv = load_x_frag(xrow + (kb + u) * 4, keep);
 #pragma unroll
-      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xv[u], acc[r]);
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xv, acc[r]);
     }
-  }
-  for (; kt < ke; ++kt) {
-    const bf16x8_t xv = load_x_frag(xrow + kt * 4, keep);
+    (void)ke;
+  } else {
+    constexpr int R = 8 / RBW;
+    int kt = kb;
+    for (; kt + R <= ke; kt += R) {
+      bf16x8_t xv[R];
+      bf16x8_t wv[R][RBW];
 #pragma unroll
-    for (int r = 0; r < RBW; ++r) acc[r] = mfma16(load_weight_tile(wt + ((size_t)r * KT + kt) * 64), xv, acc[r]);
+      for (int u = 0; u < R; ++u) {
+        xv[u] = load_x_frag(xrow + (kt + u) * 4, keep);
+#pragma unroll
+        for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kt + u) * 64);
+      }
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+#pragma unroll
+        for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xv[u], acc[r]);
+      }
+    }
+    for (; kt < ke; ++kt) {
+      const bf16x8_t xv = load_x_frag(xrow + kt * 4, keep);
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(load_weight_tile(wt + ((size_t)r * KT + kt) * 64), xv, acc[r]);
+    }
   }
 }
 
@@ -125,13 +149,9 @@ __device__ __forceinline__ bool reduce_waves(f32x4_t (&acc)[RBW], int wave, int 
   }
 }
 
-template <int RBW>
-constexpr int unroll_for() {
-  return RBW == 1 ? 8 : (RBW == 2 ? 4 : 2);
-}
-
-// y = epilogue(x . W^T) for M <= 16.  Grid: (NB / RBW) workgroups of NW waves.
-template <int NW, int RBW, int EPI>
+// y = epilogue(x . W^T) for M <= 16.  Grid: (NB / RBW) workgroups of NW waves;
+// U > 0 requires K/32 == NW * U (single-round loads).
+template <int NW, int RBW, int EPI, int U>
 __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, __bf16* __restrict__ y,
     int ldy, const __bf16* __restrict__ residual, int ldr, int M, int KT) {
@@ -152,7 +172,7 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
-  accumulate_rows<RBW, unroll_for<RBW>()>(acc, wt, xrow, m_active, KT, kb, ke);
+  accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
 
   if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
   if (!m_active) return;
@@ -185,7 +205,7 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 
 // lm_head scores for RBW row-blocks (vocab rows) + the workgroup's argmax.
 // Grid: (NB / RBW) workgroups; partial[m * P + blockIdx.x] = best (score, index).
-template <int NW, int RBW>
+template <int NW, int RBW, int U>
 __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, float* __restrict__ logits,
     int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, int M, int KT) {
@@ -203,7 +223,7 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
   for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
-  accumulate_rows<RBW, unroll_for<RBW>()>(acc, wt, xrow, m_active, KT, kb, ke);
+  accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
 
   if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
 
@@ -243,30 +263,44 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
 
 // Second stage: one workgroup per activation row reduces the P partials,
 // as the host-side torch.argmax over tile maxima does in
-// src/leanstack/runtime/cutile_logits.py:67-69.
-__global__ __launch_bounds__(256) void argmax_finalize_kernel(const ArgmaxPartial* __restrict__ partial,
-                                                              int P, long long* __restrict__ out_idx) {
+// src/leanstack/runtime/cutile_logits.py:67-69.  Each thread issues all of
+// its partial loads before comparing, so the stage costs about one memory
+// latency.
+constexpr int kFinalizeThreads = 1024;
+constexpr int kFinalizePerThread = 8;
+
+__device__ __forceinline__ void better_of(float& best, int& best_idx, float s, int i) {
+  if (s > best || (s == best && i < best_idx)) {
+    best = s;
+    best_idx = i;
+  }
+}
+
+__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const ArgmaxPartial* __restrict__ partial,
+                                                                           int P, long long* __restrict__ out_idx) {
   const int m = blockIdx.x;
+  const ArgmaxPartial* row = partial + (size_t)m * P;
   float best = -__builtin_huge_valf();
   int best_idx = INT_MAX;
-  for (int p = threadIdx.x; p < P; p += blockDim.x) {
-    const ArgmaxPartial c = partial[(size_t)m * P + p];
-    if (c.score > best || (c.score == best && c.index < best_idx)) {
-      best = c.score;
-      best_idx = c.index;
+  for (int base = 0; base < P; base += kFinalizeThreads * kFinalizePerThread) {
+    ArgmaxPartial c[kFinalizePerThread];
+#pragma unroll
+    for (int j = 0; j < kFinalizePerThread; ++j) {
+      const int p = base + j * kFinalizeThreads + (int)threadIdx.x;
+      c[j] = p < P ? row[p] : ArgmaxPartial{-__builtin_huge_valf(), INT_MAX};
     }
+#pragma unroll
+    for (int j = 0; j < kFinalizePerThread; ++j) better_of(best, best_idx, c[j].score, c[j].index);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float os = __shfl_xor(best, off);
     const int oi = __shfl_xor(best_idx, off);
-    if (os > best || (os == best && oi < best_idx)) {
-      best = os;
-      best_idx = oi;
-    }
+    better_of(best, best_idx, os, oi);
   }
-  __shared__ float s_best[4];
-  __shared__ int s_idx[4];
+  constexpr int kW = kFinalizeThreads / 64;
+  __shared__ float s_best[kW];
+  __shared__ int s_idx[kW];
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     s_best[wave] = best;
@@ -274,26 +308,48 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const ArgmaxPartia
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 4; ++w) {
-      if (s_best[w] > best || (s_best[w] == best && s_idx[w] < best_idx)) {
-        best = s_best[w];
-        best_idx = s_idx[w];
-      }
-    }
+    for (int w = 1; w < kW; ++w) better_of(best, best_idx, s_best[w], s_idx[w]);
     out_idx[m] = best_idx;
   }
 }
 
-constexpr int kLmHeadWaves = 4;
+constexpr int kLmHeadWaves = 8;
 constexpr int kLmHeadRBW = 2;
 
-template <int NW, int RBW, int EPI>
+template <int NW, int RBW, int EPI, int U>
 hipError_t launch_decode_cfg(const void* w, int NB, int KT, const void* x, int M, int ldx, void* y,
                              int ldy, const void* residual, int ldr, hipStream_t stream) {
-  decode_linear_kernel<NW, RBW, EPI><<<dim3(NB / RBW), dim3(NW * 64), 0, stream>>>(
+  decode_linear_kernel<NW, RBW, EPI, U><<<dim3(NB / RBW), dim3(NW * 64), 0, stream>>>(
       static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
       static_cast<const __bf16*>(residual), ldr, M, KT);
   return hipGetLastError();
+}
+
+// Shape dispatch: the Qwen3-4B K values get single-round instantiations
+// (K/32 = 80 -> 8 waves x 10, 128 -> 8 x 16, 304 -> 16 x 19, each measured
+// faster than the round-based loop on MI355X); any other K, and the gate/up
+// pairs, run the round-based variant.
+template <int RBW, int EPI>
+hipError_t launch_decode_shape(const void* w, int NB, int KT, const void* x, int M, int ldx, void* y, int ldy,
+                               const void* residual, int ldr, hipStream_t stream) {
+  switch (KT) {
+    case 80:
+      // The fused gate/up pair keeps the round-based loop: its single-round
+      // variant needs 96 VGPRs, which leaves 96 of its 608 workgroups for a
+      // second wave on the device.
+      if constexpr (RBW == 1) return launch_decode_cfg<8, RBW, EPI, 10>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      break;
+    case 128:
+      if constexpr (RBW == 1) return launch_decode_cfg<8, RBW, EPI, 16>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      break;
+    case 304:
+      if constexpr (RBW == 1) return launch_decode_cfg<16, RBW, EPI, 19>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      break;
+    default:
+      break;
+  }
+  if (KT >= 256) return launch_decode_cfg<16, RBW, EPI, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+  return launch_decode_cfg<8, RBW, EPI, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
 }
 
 }  // namespace
@@ -304,16 +360,12 @@ hipError_t launch_decode_linear(const void* w, int N, int K, const void* x, int 
   const int KT = K / kTileK;
   switch (epi) {
     case Epilogue::kSiluMul:
-      return launch_decode_cfg<8, 2, 1>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      return launch_decode_shape<2, 1>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
     case Epilogue::kResidualAdd:
-      if (KT >= 256)
-        return launch_decode_cfg<16, 1, 2>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
-      return launch_decode_cfg<8, 1, 2>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      return launch_decode_shape<1, 2>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
     case Epilogue::kNone:
     default:
-      if (KT >= 256)
-        return launch_decode_cfg<16, 1, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
-      return launch_decode_cfg<8, 1, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      return launch_decode_shape<1, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
   }
 }
 
@@ -325,12 +377,18 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
   const int NB = V / kTileRows;
   const int KT = K / kTileK;
   const int P = NB / kLmHeadRBW;
-  lm_head_kernel<kLmHeadWaves, kLmHeadRBW><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
-      static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
-      KT);
+  if (KT == 80) {
+    lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
+        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+        KT);
+  } else {
+    lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 0><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
+        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+        KT);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  argmax_finalize_kernel<<<dim3(M), dim3(256), 0, stream>>>(partials, P, out_idx);
+  argmax_finalize_kernel<<<dim3(M), dim3(kFinalizeThreads), 0, stream>>>(partials, P, out_idx);
   return hipGetLastError();
 }
 

@@ -22,6 +22,44 @@ constexpr int kGemmBN = 128;
 constexpr int kGemmBM = 128;
 constexpr int kGemmBK = 64;
 
+// Persistent decode-step kernel (stack.hip).
+constexpr int kStackWaves = 8;        // waves per workgroup (they split K)
+constexpr int kStackWsError = 0;      // workspace word: nonzero after a bounded wait gave up
+constexpr int kStackWsExit = 1;       // workspace word: workgroups finished (reset by the last)
+constexpr int kStackWsCounters = 16;  // workspace words from here: done[p], items published
+constexpr unsigned kStackMagic = 0x4c534b31u;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// One projection of a stack program, as the kernel reads it (64 bytes).
+struct StackDesc {
+  const bf16x8_t* w;
+  const __bf16* x;
+  __bf16* y;
+  const __bf16* res;
+  int KT, ldx, ldy, ldr;
+  int epi;         // Epilogue
+  int rbw;         // row-blocks per item: 1, or 2 for a SiLU gate/up pair
+  int items;       // work items (row-block groups) of this projection
+  int item_begin;  // global index of its first item
+  int dep;         // -1, or: every projection <= dep must finish first
+  int pad[3];
+};
+
+struct StackProgram {
+  int count;
+  int M;
+  int total_items;
+  unsigned magic;
+  int pad[12];
+  StackDesc desc[1];  // `count` entries follow the header
+};
+
+hipError_t launch_decode_stack(const StackProgram* prog, unsigned* ws, int grid, size_t lds_bytes,
+                               hipStream_t stream);
+size_t stack_lds_bytes();
+const void* stack_kernel_symbol();
+
 // Argmax partial written by each lm_head workgroup: (score, index).
 struct ArgmaxPartial {
   float score;

@@ -9,6 +9,8 @@ another implementation: a missing library or a rejected argument raises.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -115,3 +117,60 @@ def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: i
     )
     _lib.check(status, "lsk_lm_head_argmax_bf16")
     return out
+
+
+class StackStep:
+    """A prepared stack program: many projections at the same M in one
+    persistent launch (lsk_stack_prepare / lsk_stack_run).
+
+    `projections` is a list of dicts with keys x, weight (PackedWeight), out,
+    and optionally epilogue, residual, depends_on (index of an earlier entry:
+    every entry up to it finishes before this one reads its inputs)."""
+
+    def __init__(self, projections: list[dict], m: int, device: torch.device | str) -> None:
+        lib = _lib.load()
+        count = len(projections)
+        arr = (_lib.Projection * count)()
+        self._keep = []  # tensors whose pointers the program holds
+        for i, spec in enumerate(projections):
+            w = spec["weight"]
+            if not isinstance(w, PackedWeight):
+                raise ValueError(f"projection {i}: weight must be a PackedWeight")
+            x, out = spec["x"], spec["out"]
+            epi = spec.get("epilogue", _lib.EPI_NONE)
+            x2, xm, ldx = _rows(x, w.k, f"projection {i} x")
+            if xm != m:
+                raise ValueError(f"projection {i}: x has {xm} rows, the step runs M={m}")
+            n_out = w.n // 2 if epi == _lib.EPI_SILU_MUL else w.n
+            if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or out.reshape(-1, n_out).shape[0] != m:
+                raise ValueError(f"projection {i}: out must be bfloat16 [{m}, {n_out}]")
+            o2 = out.reshape(-1, n_out)
+            ldy = o2.stride(0) if m > 1 else n_out
+            res = spec.get("residual")
+            res_ptr, ldr = None, 0
+            if res is not None:
+                r2, rm, ldr = _rows(res, w.n, f"projection {i} residual")
+                res_ptr = r2.data_ptr()
+                self._keep.append(r2)
+            self._keep += [x2, o2, w.data]
+            arr[i] = _lib.Projection(w.data.data_ptr(), w.layout, w.n, w.k, x2.data_ptr(), ldx, o2.data_ptr(), ldy,
+                                     epi, res_ptr, ldr, int(spec.get("depends_on", -1)))
+        self.count = count
+        self.m = m
+        self.program = torch.empty(lib.lsk_stack_program_bytes(count), dtype=torch.uint8, device=device)
+        self.workspace = torch.zeros(lib.lsk_stack_workspace_bytes(count), dtype=torch.uint8, device=device)
+        _lib.check(lib.lsk_stack_prepare(arr, count, m, self.program.data_ptr(), self.program.numel()),
+                   "lsk_stack_prepare")
+
+    def launch(self) -> None:
+        lib = _lib.load()
+        _lib.check(lib.lsk_stack_run(self.program.data_ptr(), self.count, self.workspace.data_ptr(),
+                                     self.workspace.numel(), stream_handle()), "lsk_stack_run")
+
+    def error(self) -> int:
+        """Read and clear the error word (synchronises): 0 if every wait completed."""
+        lib = _lib.load()
+        torch.cuda.synchronize(self.workspace.device)
+        out = ctypes.c_int(0)
+        _lib.check(lib.lsk_stack_error(self.workspace.data_ptr(), ctypes.byref(out)), "lsk_stack_error")
+        return out.value

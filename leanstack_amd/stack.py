@@ -1,0 +1,110 @@
+"""The decode step's projection sequence over all resident layers.
+
+Per layer, in the reference's call order (src/leanstack/runtime/qwen_explicit.py:
+1247-1272 for M = 1, :1211-1244 for the verify batch), the step runs the fused
+QKV projection, o_proj, the fused gate_up with SiLU(gate)*up and down_proj.
+The RMSNorm / q-k norm / RoPE / attention work between them is not part of
+this path; each projection reads a fixed input buffer instead (its "fresh"
+activations), so the stack measures exactly the projection traffic of a
+decode step.  All launches go to one stream in dependency order, and the
+whole step can be captured once as a HIP graph and replayed, which takes
+host launch cost out of the step time.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, kernels
+from .geometry import QwenGeometry
+from .layout import PackedWeight
+
+
+@dataclass
+class LayerProjections:
+    qkv: PackedWeight
+    o: PackedWeight
+    gate_up: PackedWeight
+    down: PackedWeight
+
+
+class DecodeLinearStack:
+    def __init__(self, layers: list[LayerProjections], geometry: QwenGeometry, max_rows: int,
+                 device: torch.device, inputs: dict[str, torch.Tensor] | None = None) -> None:
+        if not 1 <= max_rows <= 16:
+            raise ValueError("the decode stack serves M = 1..16 rows")
+        self.layers = layers
+        self.g = geometry
+        self.max_rows = max_rows
+        self.device = device
+        n = len(layers)
+        h, q, i, qkv = geometry.hidden_size, geometry.q_dim, geometry.intermediate_size, geometry.qkv_dim
+        if inputs is None:
+            gen = torch.Generator(device=device).manual_seed(1)
+            inputs = {
+                "qkv": torch.randn((n, max_rows, h), generator=gen, device=device).to(torch.bfloat16),
+                "o": torch.randn((n, max_rows, q), generator=gen, device=device).to(torch.bfloat16),
+                "gate_up": torch.randn((n, max_rows, h), generator=gen, device=device).to(torch.bfloat16),
+            }
+        self.x_qkv, self.x_o, self.x_gu = inputs["qkv"], inputs["o"], inputs["gate_up"]
+        self.y_qkv = torch.empty((max_rows, qkv), device=device, dtype=torch.bfloat16)
+        self.y_o = torch.empty((max_rows, h), device=device, dtype=torch.bfloat16)
+        self.act = torch.empty((max_rows, i), device=device, dtype=torch.bfloat16)
+        self.y_down = torch.empty((max_rows, h), device=device, dtype=torch.bfloat16)
+
+    def launch(self, m: int, layers: range | None = None) -> None:
+        """Enqueue one step (all layers, or `layers`) at M = m rows."""
+        if not 1 <= m <= self.max_rows:
+            raise ValueError(f"m={m} outside 1..{self.max_rows}")
+        for l in layers if layers is not None else range(len(self.layers)):
+            p = self.layers[l]
+            kernels.linear(self.x_qkv[l, :m], p.qkv, out=self.y_qkv[:m])
+            kernels.linear(self.x_o[l, :m], p.o, out=self.y_o[:m])
+            kernels.linear(self.x_gu[l, :m], p.gate_up, epilogue=_lib.EPI_SILU_MUL, out=self.act[:m])
+            kernels.linear(self.act[:m], p.down, out=self.y_down[:m])
+
+    def launch_projection(self, name: str, m: int) -> None:
+        """Enqueue one projection kind across all layers (per-kernel timing)."""
+        for l, p in enumerate(self.layers):
+            if name == "qkv_proj":
+                kernels.linear(self.x_qkv[l, :m], p.qkv, out=self.y_qkv[:m])
+            elif name == "o_proj":
+                kernels.linear(self.x_o[l, :m], p.o, out=self.y_o[:m])
+            elif name == "gate_up_proj":
+                kernels.linear(self.x_gu[l, :m], p.gate_up, epilogue=_lib.EPI_SILU_MUL, out=self.act[:m])
+            elif name == "down_proj":
+                kernels.linear(self.act[:m], p.down, out=self.y_down[:m])
+            else:
+                raise ValueError(name)
+
+    def persistent_step(self, m: int, chain: bool = True) -> kernels.StackStep:
+        """The same step as launch(m) as one persistent-kernel program.  With
+        `chain`, every projection waits for all earlier ones (the decode
+        step's dependency chain: each projection's input is produced from the
+        previous one's output); weights still stream ahead of the waits."""
+        specs = []
+        for l, p in enumerate(self.layers):
+            base = len(specs)
+            dep = (lambda i: i - 1) if chain else (lambda i: -1)
+            specs.append({"x": self.x_qkv[l, :m], "weight": p.qkv, "out": self.y_qkv[:m], "depends_on": dep(base)})
+            specs.append({"x": self.x_o[l, :m], "weight": p.o, "out": self.y_o[:m], "depends_on": dep(base + 1)})
+            specs.append({"x": self.x_gu[l, :m], "weight": p.gate_up, "out": self.act[:m],
+                          "epilogue": _lib.EPI_SILU_MUL, "depends_on": dep(base + 2)})
+            specs.append({"x": self.act[:m], "weight": p.down, "out": self.y_down[:m], "depends_on": base + 2})
+        return kernels.StackStep(specs, m, self.device)
+
+    def capture(self, fn) -> torch.cuda.CUDAGraph:
+        """Capture `fn()` (a launch sequence) as a HIP graph."""
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            fn()  # warm the launch path outside capture
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        torch.cuda.synchronize(self.device)
+        return graph
