@@ -56,6 +56,20 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def measured_traffic(kernel_label: str):
+    """HBM bytes per launch of the roofline kernel, as the committed counter
+    profile measured it (profiles/hbm_traffic.json), or None."""
+    path = REPO / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    kernels = json.loads(path.read_text()).get("kernels", {})
+    for name, rec in kernels.items():
+        if kernel_label.startswith(name.split("<")[0]) and name.split("<")[1].split(">")[0].replace(" ", "") in \
+                kernel_label.replace(" ", ""):
+            return rec["traffic_bytes"]
+    return None
+
+
 def cpu_baseline(g, seconds: float) -> dict:
     """The reference's CPU torch path (torch.mv in bf16 + F.silu*mul, via the
     oracle) on this host's cores, over a bounded sample: two distinct random
@@ -107,6 +121,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="skip the prefill sweep and the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc", action="store_true",
+                    help="short run for hardware-counter profiling: a 1 GiB copy of known size, then each "
+                         "projection kind once per layer and the lm_head once, no graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
@@ -151,6 +168,21 @@ def main() -> int:
 
     stack = DecodeLinearStack(layers, G, max_rows=16, device=dev)
 
+    if args.pmc:
+        # Calibration: a plain device copy of exactly 1 GiB (read 1 GiB, write 1 GiB).
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        for name in G.projections():
+            stack.launch_projection(name, 1)
+        hidden = torch.randn((1, G.hidden_size), generator=gen, device=dev).to(torch.bfloat16)
+        kernels.lm_head_argmax(hidden, lm_head)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_run": True, "copy_bytes": 2 * src.numel(),
+                          "bytes_per_launch": {n: G.projection_bytes(n, 1) for n in G.projections()}}), flush=True)
+        return 0
+
     # --- headline: 36-layer decode step, verify sweep -----------------------
     # (a) 144 projection launches captured in one HIP graph;
     # (b) the persistent stack kernel: one launch per step, every projection
@@ -172,7 +204,10 @@ def main() -> int:
         del graph, prog
     if stack_errors:
         raise SystemExit(f"persistent stack kernel reported {stack_errors} failed waits")
-    ms_step = sweep[1]
+    # The headline step path is whichever product path is faster at M = 1.
+    persistent_is_faster = sweep[1] < sweep_launches[1]
+    headline = sweep if persistent_is_faster else sweep_launches
+    ms_step = headline[1]
     value = G.stack_bytes(1) / (ms_step * 1e-3) / 1e9
 
     # --- per projection kind: 36 launches of one kind per replay ------------
@@ -188,9 +223,17 @@ def main() -> int:
         }
         log(f"{name} M=1: {us:.2f} us/launch, {per_kernel[name]['GB/s']} GB/s")
         del graph
-    # The dominant (and only) kernel of the step is the persistent stack kernel:
-    # one launch moves the step's 7.27 GB; its launch duration is the step time.
-    achieved = value
+    if persistent_is_faster:
+        # One launch moves the step's 7.27 GB; its duration is the step time.
+        roof_kernel = "decode_stack_kernel (one launch = 36-layer step at M=1)"
+        roof_bytes = G.stack_bytes(1)
+        achieved = value
+    else:
+        # Dominant kernel of the launch graph: the fused gate_up + SiLU*up
+        # decode kernel (49% of the step's bytes), timed over 36 launches.
+        roof_kernel = "decode_linear_kernel<8,2,1,0> (gate_up 19456x2560 + silu*up, M=1)"
+        roof_bytes = G.projection_bytes("gate_up_proj", 1)
+        achieved = roof_bytes / (per_kernel["gate_up_proj"]["us_per_launch"] * 1e-6) / 1e9
 
     # --- lm_head + argmax ------------------------------------------------------
     head = {}
@@ -250,8 +293,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations, generated on the GPU)",
         "config": {
             "workload": "qwen3-4b decode projection stack: 36 layers x (qkv 6144x2560, o 2560x4096, "
-                        "gate_up 19456x2560 + silu*up, down 2560x9728), M=1, one persistent kernel per step, "
-                        "each projection waiting for the previous one",
+                        "gate_up 19456x2560 + silu*up, down 2560x9728), M=1, each projection after the previous one",
             "layers": G.num_hidden_layers,
             "m": 1,
             "bytes_per_step": G.stack_bytes(1),
@@ -259,20 +301,24 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_stack_kernel (one launch = 36-layer step at M=1)",
-            "bytes_per_launch": G.stack_bytes(1),
+            "kernel": roof_kernel,
+            "bytes_per_launch": roof_bytes,
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(roof_kernel),
+            "traffic_source": "profiles/decode_projections_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                              "scaled by a 1 GiB copy in the same run)",
         },
         "cpu_baseline": cpu,
         "detail": {
             "stack_frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-            "verify_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep.items()},
-            "verify_ratio_vs_m1": {str(m): round(v / sweep[1], 4) for m, v in sweep.items()},
+            "step_path": "persistent stack kernel" if persistent_is_faster else "HIP graph of 144 projection launches",
+            "verify_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in headline.items()},
+            "verify_ratio_vs_m1": {str(m): round(v / headline[1], 4) for m, v in headline.items()},
             "launches_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep_launches.items()},
+            "persistent_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep.items()},
             "per_projection_m1": per_kernel,
             "lm_head_argmax": {str(m): v for m, v in head.items()},
             "prefill": {str(m): v for m, v in prefill.items()},

@@ -4,8 +4,9 @@ leanstack's semantic runtime calls these module-level names once per layer
 per step (src/leanstack/runtime/qwen_explicit.py:963-971, call sites :1117,
 :1155, :1170, :1235, :1264, :1293).  Here every projection inside them runs
 on the gfx950 kernels through the C ABI; the work around the projections
-that is not part of this path (RMSNorm, q/k norm, RoPE, SDPA) stays the same
-torch ops the reference uses.  The weight arguments are PackedWeight objects
+that is not part of this path (RMSNorm, q/k norm, RoPE, attention) stays
+torch code with the reference's semantics (attention is computed explicitly
+in fp32 with contiguous operands, see _sdpa).  The weight arguments are PackedWeight objects
 from the resident arena (leanstack_amd.leanserve) instead of row-major
 tensors; a row-major tensor is rejected with ValueError.
 
@@ -55,9 +56,18 @@ def qwen_apply_rotary_pos_emb(query_states, key_states, cos, sin, unsqueeze_dim:
 
 
 def _sdpa(query_states, key_states, value_states, attention_scale, num_key_value_groups):
-    kwargs = {"enable_gqa": True} if num_key_value_groups > 1 else {}
-    return F.scaled_dot_product_attention(query_states, key_states, value_states, dropout_p=0.0, is_causal=False,
-                                          scale=attention_scale, **kwargs)
+    """Non-causal GQA attention with the semantics of the reference's
+    F.scaled_dot_product_attention call (qwen_explicit.py:894-912), computed
+    in fp32 with contiguous operands: softmax(q k^T * scale) v, kv heads
+    repeated per group, result in the query dtype."""
+    k = key_states.float()
+    v = value_states.float()
+    if num_key_value_groups > 1:
+        k = k.repeat_interleave(num_key_value_groups, dim=1)
+        v = v.repeat_interleave(num_key_value_groups, dim=1)
+    scores = torch.matmul(query_states.float(), k.transpose(-2, -1).contiguous()) * attention_scale
+    probs = torch.softmax(scores, dim=-1)
+    return torch.matmul(probs, v.contiguous()).to(query_states.dtype)
 
 
 def _require_packed(weight, what: str, layout: int = _lib.LAYOUT_MFMA16X32) -> PackedWeight:

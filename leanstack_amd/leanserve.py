@@ -15,6 +15,7 @@ resident with room to spare.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from pathlib import Path
 from math import ceil
 from typing import Iterable
 
@@ -244,9 +245,9 @@ class ResidentArena:
     def __init__(self, plan: ResidentBufferPlan, device: torch.device | str) -> None:
         self.plan = plan
         self.device = torch.device(device)
-        self.buffer = torch.empty(plan.arena_bytes, dtype=torch.uint8, device=self.device)
-        if self.buffer.data_ptr() % 256:
-            raise RuntimeError("arena base is not 256-byte aligned")
+        raw = torch.empty(plan.arena_bytes + 256, dtype=torch.uint8, device=self.device)
+        skew = (-raw.data_ptr()) % 256  # device allocations are aligned already; host ones may not be
+        self.buffer = raw[skew : skew + plan.arena_bytes]
         self._index = {e.name: e for e in plan.entries}
 
     def view(self, name: str) -> torch.Tensor:
@@ -278,3 +279,86 @@ class ResidentArena:
         if e.layout is None or packed.numel() * 2 != e.nbytes:
             raise ValueError(f"{name}: not a packed entry of {e.nbytes} bytes")
         self.buffer[e.offset : e.end].view(torch.bfloat16).copy_(packed.reshape(-1))
+
+
+# ----------------------------------------------------------------- loading
+
+
+def materialize_qwen_semantic_stack_from_leanpack(
+    pack_dir: str | Path,
+    *,
+    device: str | torch.device = "cuda:0",
+    include_output_head: bool = True,
+    max_rows: int = 16,
+    buckets: Iterable[BucketSpec] = DEFAULT_BUCKETS,
+):
+    """Load a leanpack/v1 artifact into one resident arena and build the
+    runtime (replaces src/leanstack/leanserve.py:470-530, which copies each
+    tensor to its own allocation).  Returns (runtime, arena)."""
+    from safetensors import safe_open
+
+    from .pack import geometry_from_manifest, load_packed_artifact_manifest
+    from .runtime import (
+        QwenSemanticAttentionRuntime,
+        QwenSemanticLayerRuntime,
+        QwenSemanticMlpRuntime,
+        QwenSemanticStackRuntime,
+        QwenServeConfig,
+        split_rows,
+    )
+
+    root = Path(pack_dir)
+    manifest = load_packed_artifact_manifest(root)
+    g = geometry_from_manifest(manifest)
+    plan = build_resident_buffer_plan(g, buckets=buckets, max_rows=max_rows, include_lm_head=include_output_head)
+    arena = ResidentArena(plan, device)
+    planned = {e.name for e in plan.entries}
+    by_file: dict[str, list] = {}
+    for t in manifest.tensors:
+        if t.name in planned:
+            by_file.setdefault(t.file, []).append(t)
+    for file_name, entries in by_file.items():
+        with safe_open(str(root / file_name), framework="pt", device="cpu") as handle:
+            for t in entries:
+                value = handle.get_tensor(t.name)
+                if t.layout == "rowmajor":
+                    arena.view(t.name).copy_(value.view(arena.plan.entry(t.name).shape))
+                else:
+                    arena.store_packed(t.name, value)
+
+    cfg = QwenServeConfig(
+        vocab_size=g.vocab_size, hidden_size=g.hidden_size, intermediate_size=g.intermediate_size,
+        num_hidden_layers=g.num_hidden_layers, num_attention_heads=g.num_attention_heads,
+        num_key_value_heads=g.num_key_value_heads, max_position_embeddings=g.max_position_embeddings,
+        head_dim=g.head_dim, rms_norm_eps=g.rms_norm_eps, rope_parameters={"rope_theta": g.rope_theta},
+    )
+    layers = []
+    for layer in range(g.num_hidden_layers):
+        n = layer_entry_names(layer)
+        qkv = arena.packed(n["qkv_proj"])
+        q, k, v = split_rows(qkv, (g.q_dim, g.kv_dim, g.kv_dim))
+        attention = QwenSemanticAttentionRuntime(
+            layer_idx=layer, q_proj_weight=q, k_proj_weight=k, v_proj_weight=v, qkv_proj_weight=qkv,
+            q_proj_out_dim=g.q_dim, k_proj_out_dim=g.kv_dim, num_attention_heads=g.num_attention_heads,
+            num_key_value_heads=g.num_key_value_heads,
+            num_key_value_groups=g.num_attention_heads // g.num_key_value_heads, head_dim=g.head_dim,
+            attention_scale=g.head_dim ** -0.5, o_proj_weight=arena.packed(n["o_proj"]),
+            q_norm_weight=arena.view(n["q_norm"]), k_norm_weight=arena.view(n["k_norm"]),
+        )
+        mlp = QwenSemanticMlpRuntime(gate_up_proj_weight=arena.packed(n["gate_up_proj"]),
+                                     gate_proj_out_dim=g.intermediate_size,
+                                     down_proj_weight=arena.packed(n["down_proj"]))
+        layers.append(QwenSemanticLayerRuntime(
+            layer_idx=layer, input_layernorm_weight=arena.view(n["input_layernorm"]), attention=attention,
+            post_attention_layernorm_weight=arena.view(n["post_attention_layernorm"]), mlp=mlp))
+    dev = torch.device(device)
+    inv_freq = 1.0 / (g.rope_theta ** (torch.arange(0, g.head_dim, 2, device=dev, dtype=torch.float32) / g.head_dim))
+    runtime = QwenSemanticStackRuntime(
+        model_path=root, config=cfg, layer_indices=tuple(range(g.num_hidden_layers)),
+        embed_tokens_weight=arena.view("model.embed_tokens.weight"), layers=tuple(layers),
+        rope_inv_freq=inv_freq, attention_scaling=1.0,
+        final_norm_weight=arena.view("model.norm.weight") if include_output_head else None,
+        lm_head_weight=arena.packed("lm_head.weight") if include_output_head else None,
+        device=dev, dtype=torch.bfloat16,
+    )
+    return runtime, arena

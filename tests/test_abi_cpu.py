@@ -1,0 +1,116 @@
+"""The C ABI without a GPU: the library loads, exports every declared symbol,
+and rejects bad arguments before anything touches the device."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from leanstack_amd import _lib
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+def test_library_exports_every_header_function():
+    lib = _lib.load()
+    names = _lib.header_functions()
+    assert {"lsk_linear_bf16", "lsk_lm_head_argmax_bf16", "lsk_pack_bf16", "lsk_stack_run"} <= set(names)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing
+    assert set(names) == set(_lib._SIGNATURES)  # every export has declared ctypes types
+    assert lib.lsk_abi_version() == _lib.ABI_VERSION
+
+
+def test_projection_struct_layout():
+    # struct lsk_projection on x86-64 (natural alignment, 8-byte pointers)
+    assert ctypes.sizeof(_lib.Projection) == 72
+    assert _lib.Projection.x.offset == 24 and _lib.Projection.y.offset == 40
+    assert _lib.Projection.residual.offset == 56 and _lib.Projection.depends_on.offset == 68
+
+
+FAKE = 0x10000  # a 64 KiB-aligned non-null address: never dereferenced, calls fail validation first
+
+
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(layout=9), _lib.ERR_LAYOUT),
+    (dict(n=2568), _lib.ERR_INVALID),        # N not a multiple of 16
+    (dict(k=2576), _lib.ERR_INVALID),        # K not a multiple of 32
+    (dict(m=0), _lib.ERR_INVALID),
+    (dict(ldx=2552), _lib.ERR_INVALID),      # ldx < K
+    (dict(ldx=2564), _lib.ERR_INVALID),      # ldx not a multiple of 8
+    (dict(epi=1), _lib.ERR_INVALID),         # SiLU needs the gate_up layout
+    (dict(epi=5), _lib.ERR_INVALID),
+    (dict(epi=2), _lib.ERR_INVALID),         # residual-add without a residual
+    (dict(x=0), _lib.ERR_INVALID),
+    (dict(x=FAKE + 2), _lib.ERR_INVALID),    # x misaligned
+    (dict(ldy=6142), _lib.ERR_INVALID),      # ldy < N
+])
+def test_linear_rejects_before_launch(kwargs, code):
+    a = dict(w=FAKE, layout=1, n=6144, k=2560, x=FAKE, m=1, ldx=2560, y=FAKE, ldy=6144, epi=0, res=None, ldr=0)
+    a.update(kwargs)
+    lib = _lib.load()
+    status = lib.lsk_linear_bf16(a["w"], a["layout"], a["n"], a["k"], a["x"] or None, a["m"], a["ldx"], a["y"],
+                                 a["ldy"], a["epi"], a["res"], a["ldr"], None, 0, None)
+    assert status == code, _lib.last_error()
+    assert _lib.last_error()
+    with pytest.raises(ValueError):
+        _lib.check(status, "lsk_linear_bf16")
+
+
+def test_lm_head_rejects_before_launch():
+    lib = _lib.load()
+    ok = dict(V=151936, K=2560, M=1)
+    ws = lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 1, 151936, 2560)
+    assert ws == (151936 // 32) * 8
+    cases = [
+        (dict(M=17), _lib.ERR_INVALID),
+        (dict(V=151920), _lib.ERR_INVALID),   # V % 32 != 0
+        (dict(mode=3), _lib.ERR_INVALID),
+        (dict(ws=ws - 8), _lib.ERR_WORKSPACE),
+        (dict(layout=2), _lib.ERR_LAYOUT),
+    ]
+    for over, code in cases:
+        a = dict(ok, mode=0, ws=ws, layout=1)
+        a.update(over)
+        st = lib.lsk_lm_head_argmax_bf16(FAKE, a["layout"], a["V"], a["K"], FAKE, a["M"], 2560, None, a["mode"], FAKE,
+                                         FAKE, a["ws"], None)
+        assert st == code, (over, _lib.last_error())
+
+
+def test_stack_prepare_rejects_bad_programs():
+    lib = _lib.load()
+    good = _lib.Projection(FAKE, 1, 6144, 2560, FAKE, 2560, FAKE, 6144, 0, None, 0, -1)
+    prog_bytes = lib.lsk_stack_program_bytes(2)
+    assert lib.lsk_stack_workspace_bytes(144) % 256 == 0
+
+    def prepare(*projs, m=1, nbytes=prog_bytes):
+        arr = (_lib.Projection * len(projs))(*projs)
+        return lib.lsk_stack_prepare(arr, len(projs), m, FAKE, nbytes)
+
+    self_dep = _lib.Projection(FAKE, 1, 6144, 2560, FAKE, 2560, FAKE, 6144, 0, None, 0, 1)
+    assert prepare(good, self_dep) == _lib.ERR_INVALID
+    assert prepare(good, good, m=17) == _lib.ERR_INVALID
+    assert prepare(good, good, nbytes=prog_bytes - 1) == _lib.ERR_INVALID
+    k_small = _lib.Projection(FAKE, 1, 64, 128, FAKE, 128, FAKE, 64, 0, None, 0, -1)
+    assert prepare(good, k_small) == _lib.ERR_INVALID  # K/32 = 4 < 8 waves
+    assert "projection 1" in _lib.last_error()
+    assert lib.lsk_stack_run(FAKE, 2, FAKE, 16, None) == _lib.ERR_WORKSPACE
+
+
+def test_bench_refuses_more_than_one_gpu():
+    out = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120)
+    assert out.returncode == 2
+    assert "one GPU" in json.loads(out.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_product_package_does_not_import_the_oracle():
+    for path in (REPO / "leanstack_amd").rglob("*.py"):
+        text = path.read_text(encoding="utf-8")
+        assert "import oracle" not in text and "from oracle" not in text, path

@@ -1,0 +1,111 @@
+"""leanpack/v1: pack a synthetic Qwen3 checkpoint, validate the manifest, and
+materialize it into the resident arena (CPU here; the GPU variant runs the
+dispatch entry points on a real-shape layer)."""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+import torch
+
+from leanstack_amd import _lib
+from leanstack_amd.geometry import QwenGeometry
+from leanstack_amd.leanserve import materialize_qwen_semantic_stack_from_leanpack
+from leanstack_amd.pack import (
+    FORMAT_VERSION,
+    build_qwen_leanpack,
+    hf_layer_names,
+    load_packed_artifact_manifest,
+    synthetic_qwen_checkpoint,
+)
+
+TINY = QwenGeometry(num_hidden_layers=2, hidden_size=256, intermediate_size=512, num_attention_heads=4,
+                    num_key_value_heads=2, head_dim=64, vocab_size=1024)
+
+
+@pytest.fixture(scope="module")
+def tiny_pack(tmp_path_factory):
+    ckpt = synthetic_qwen_checkpoint(TINY, seed=3)
+    out = tmp_path_factory.mktemp("pack")
+    manifest = build_qwen_leanpack(ckpt, out, geometry=TINY)
+    return ckpt, out, manifest
+
+
+def test_manifest_layout_and_geometry(tiny_pack):
+    _, out, manifest = tiny_pack
+    assert manifest.format_version == FORMAT_VERSION
+    assert manifest.layout["tile_rows"] == 16 and manifest.layout["tile_k"] == 32
+    assert manifest.layout["target_gpu"].startswith("MI355X")
+    assert manifest.geometry["num_hidden_layers"] == 2
+    assert [f.file for f in manifest.files] == ["embeddings.safetensors", "layer-000.safetensors",
+                                                "layer-001.safetensors", "output.safetensors"]
+    t = manifest.tensor("layers.1.attention.qkv_proj.weight")
+    assert t.layout == "mfma16x32" and t.logical_shape == [512, 256] and t.shape == [512 * 256]
+    assert t.source_tensors == ["model.layers.1.self_attn.q_proj.weight", "model.layers.1.self_attn.k_proj.weight",
+                                "model.layers.1.self_attn.v_proj.weight"]
+    assert manifest.tensor("layers.0.mlp.gate_up_proj.weight").layout == "mfma16x32_gateup"
+    assert manifest.tensor("lm_head.weight").source_tensors == ["model.embed_tokens.weight"]  # tied head
+    reread = load_packed_artifact_manifest(out)
+    assert reread.tensors == manifest.tensors
+
+
+def test_loader_refuses_other_formats(tiny_pack, tmp_path):
+    _, out, _ = tiny_pack
+    payload = json.loads((out / "manifest.json").read_text())
+    bad = tmp_path / "v0"
+    bad.mkdir()
+    (bad / "manifest.json").write_text(json.dumps(dict(payload, format_version="leanpack/v0")))
+    with pytest.raises(ValueError):
+        load_packed_artifact_manifest(bad)
+    payload["tensors"][1]["layout"] = "tiles64x64"
+    (bad / "manifest.json").write_text(json.dumps(payload))
+    with pytest.raises(ValueError):
+        load_packed_artifact_manifest(bad)
+
+
+def test_materialize_round_trips_every_tensor(tiny_pack):
+    ckpt, out, _ = tiny_pack
+    runtime, arena = materialize_qwen_semantic_stack_from_leanpack(out, device="cpu", buckets=())
+    assert torch.equal(runtime.embed_tokens_weight, ckpt["model.embed_tokens.weight"])
+    assert torch.equal(runtime.lm_head_weight.unpack(), ckpt["model.embed_tokens.weight"])
+    for layer, lr in enumerate(runtime.layers):
+        n = hf_layer_names(layer)
+        att, mlp = lr.attention, lr.mlp
+        assert torch.equal(att.q_proj_weight.unpack(), ckpt[n["q_proj"]])
+        assert torch.equal(att.k_proj_weight.unpack(), ckpt[n["k_proj"]])
+        assert torch.equal(att.v_proj_weight.unpack(), ckpt[n["v_proj"]])
+        assert torch.equal(att.o_proj_weight.unpack(), ckpt[n["o_proj"]])
+        fused = torch.cat((ckpt[n["gate_proj"]], ckpt[n["up_proj"]]))
+        assert torch.equal(mlp.gate_up_proj_weight.unpack(), fused)
+        assert mlp.gate_up_proj_weight.layout == _lib.LAYOUT_MFMA16X32_GATEUP
+        assert torch.equal(mlp.down_proj_weight.unpack(), ckpt[n["down_proj"]])
+        assert torch.equal(lr.input_layernorm_weight, ckpt[n["input_layernorm"]])
+        assert torch.equal(att.k_norm_weight, ckpt[n["k_norm"]])
+        # views share the arena: one allocation holds everything
+        assert att.qkv_proj_weight.data.untyped_storage().data_ptr() == arena.buffer.untyped_storage().data_ptr()
+    assert runtime.config.num_key_value_heads == 2 and runtime.layers[0].attention.num_key_value_groups == 2
+
+
+@pytest.mark.gpu
+def test_real_shape_layer_from_pack_runs_the_dispatch_path(gpu, tmp_path):
+    from leanstack_amd import dispatch
+    from oracle import projections as ref
+    from tests.helpers import activations, assert_parity
+
+    g = QwenGeometry(num_hidden_layers=1, vocab_size=4096)
+    ckpt = synthetic_qwen_checkpoint(g, seed=9)
+    build_qwen_leanpack(ckpt, tmp_path / "pack", geometry=g)
+    runtime, _ = materialize_qwen_semantic_stack_from_leanpack(tmp_path / "pack", device="cuda:0", buckets=())
+    lr = runtime.layers[0]
+    n = hf_layer_names(0)
+    h = activations(1, g.hidden_size, seed=4).view(-1)
+    y = dispatch._semantic_mlp_epilogue_vector(h.cuda(), lr.post_attention_layernorm_weight, lr.mlp.gate_up_proj_weight,
+                                               lr.mlp.gate_proj_out_dim, lr.mlp.down_proj_weight, g.rms_norm_eps)
+    gu = torch.cat((ckpt[n["gate_proj"]], ckpt[n["up_proj"]]))
+    expect = ref.mlp_epilogue_vector(h, ckpt[n["post_attention_layernorm"]], gu, g.intermediate_size,
+                                     ckpt[n["down_proj"]], g.rms_norm_eps)
+    assert_parity(y.cpu(), expect, "mlp from leanpack")
+    tok = dispatch.select_semantic_greedy_token(runtime, h.view(1, 1, -1).cuda())
+    normed = ref.rmsnorm(h.view(1, -1), ckpt["model.norm.weight"], g.rms_norm_eps).view(-1)
+    assert tok.item() == ref.logits_argmax(normed, ckpt["model.embed_tokens.weight"]).item()

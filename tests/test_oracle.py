@@ -1,0 +1,179 @@
+"""Pin the CPU oracle (oracle/projections.py) before trusting it.
+
+Each check is chosen so that a plausible mistake in the oracle -- a dropped
+term, a transposed operand, a wrong sign or split, a wrong rounding chain or
+tie rule -- fails it.  None of them restates the oracle's own formula.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute
+from oracle import projections as ref
+from tests.helpers import bits, from_bits
+
+
+def _case(n, k, m, seed):
+    rng = np.random.default_rng(seed)
+    w = brute.f32_to_bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = brute.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    return w, x
+
+
+def _within_rounding(got: np.ndarray, y64: np.ndarray, bound: np.ndarray) -> bool:
+    slack = 0.5 * np.maximum(brute.bf16_ulp(y64), brute.bf16_ulp(got)) + bound + 1e-30
+    return bool(np.all(np.abs(got - y64) <= slack))
+
+
+@pytest.mark.parametrize("n,k,m", [(16, 32, 1), (48, 96, 3), (64, 2560, 2), (32, 9728, 1)])
+def test_linear_matches_float64_brute_force(n, k, m):
+    w, x = _case(n, k, m, seed=n + k + m)
+    y64 = brute.linear64(x, w)
+    bound = brute.fp32_sum_bound(x, w)
+    got = ref.linear(from_bits(x), from_bits(w)).double().numpy()
+    assert _within_rounding(got, y64, bound)
+    if m == 1:
+        got_mv = ref.mv(from_bits(w), from_bits(x)[0]).double().numpy()
+        assert _within_rounding(got_mv[None, :], y64, bound)
+
+
+def test_one_hot_activation_returns_weight_column_exactly():
+    w, _ = _case(64, 128, 1, seed=3)
+    wt = from_bits(w)
+    for col in (0, 7, 64, 127):
+        x = torch.zeros(128, dtype=torch.bfloat16)
+        x[col] = 1.0
+        assert torch.equal(ref.mv(wt, x), wt[:, col])
+
+
+def test_power_of_two_scaling_is_exact():
+    w, x = _case(32, 256, 2, seed=4)
+    wt, xt = from_bits(w), from_bits(x)
+    base = ref.linear(xt, wt)
+    assert torch.equal(ref.linear(xt * 4, wt), base * 4)
+    assert torch.equal(ref.linear(xt, wt * 0.5), base * 0.5)
+
+
+def test_linearity_in_x():
+    w, x = _case(32, 512, 2, seed=5)
+    wt = from_bits(w).double()
+    a, b = from_bits(x).double()
+    ya = torch.mv(wt, a)
+    yb = torch.mv(wt, b)
+    ysum = torch.mv(wt, a + b)
+    assert torch.allclose(ysum, ya + yb, rtol=0, atol=1e-9)
+    got = ref.mv(from_bits(w), (a + b).to(torch.bfloat16)).double()
+    bf_sum_exact = (a + b).to(torch.bfloat16).double()
+    assert torch.allclose(got, torch.mv(wt, bf_sum_exact), rtol=2e-2, atol=1e-2)
+
+
+def test_rows_are_independent():
+    """M stacked GEMVs equal one GEMM (rows do not mix), to fp32-order noise."""
+    w, x = _case(64, 256, 4, seed=6)
+    wt, xt = from_bits(w), from_bits(x)
+    full = ref.linear(xt, wt).double()
+    stacked = torch.stack([ref.mv(wt, xt[i]) for i in range(4)]).double()
+    y64 = brute.linear64(x, w)
+    bound = brute.fp32_sum_bound(x, w)
+    assert _within_rounding(full.numpy(), y64, bound)
+    assert _within_rounding(stacked.numpy(), y64, bound)
+    # Permuting the rows of x permutes the rows of y: no cross-row terms.
+    perm = torch.tensor([2, 0, 3, 1])
+    assert torch.equal(ref.linear(xt[perm], wt), ref.linear(xt, wt)[perm])
+
+
+def test_fused_qkv_segment_order():
+    """One-hot weight rows pin [q | k | v] along the fused output (pack.py:271-274)."""
+    q, kv, k = 8, 4, 16
+    w = torch.zeros(q + 2 * kv, k, dtype=torch.bfloat16)
+    for r in range(q + 2 * kv):
+        w[r, r % k] = 1.0 + r  # row r reads input r % k, scaled by its own index
+    x = torch.arange(1, k + 1, dtype=torch.bfloat16)
+    y = ref.mv(w, x)
+    qs, ks, vs = torch.split(y, (q, kv, kv))
+    assert qs.tolist() == [(1.0 + r) * ((r % k) + 1) for r in range(q)]
+    assert ks.tolist() == [(1.0 + r) * ((r % k) + 1) for r in range(q, q + kv)]
+    assert vs.tolist() == [(1.0 + r) * ((r % k) + 1) for r in range(q + kv, q + 2 * kv)]
+
+
+def test_silu_mul_applies_silu_to_the_gate_half():
+    """SiLU goes on the first (gate) half, the second half multiplies
+    (qwen_explicit.py:829-830): swapping the halves changes the result."""
+    gate = torch.tensor([[0.0, 8.0, -8.0, 1.0]], dtype=torch.bfloat16)
+    up = torch.tensor([[5.0, 3.0, 3.0, 2.0]], dtype=torch.bfloat16)
+    out = ref.silu_mul(torch.cat((gate, up), dim=-1), 4).double()
+    g = gate.double().numpy()
+    u = up.double().numpy()
+    expect = brute.silu_mul_chain(g, u)
+    assert np.allclose(out.numpy(), expect, rtol=0, atol=0)
+    assert out[0, 0] == 0.0                       # silu(0) = 0
+    assert abs(out[0, 1] - 8.0 * 3.0) < 0.05 * 24  # large +g -> g * u
+    assert abs(out[0, 2]) < 0.01                  # large -g -> 0
+    swapped = ref.silu_mul(torch.cat((up, gate), dim=-1), 4)
+    assert not torch.equal(swapped, out.to(torch.bfloat16))
+
+
+def test_silu_matches_closed_form_elementwise():
+    rng = np.random.default_rng(8)
+    g = brute.round_bf16(rng.standard_normal(4096) * 4)
+    u = brute.round_bf16(rng.standard_normal(4096))
+    gt = torch.tensor(g, dtype=torch.float64).to(torch.bfloat16)
+    ut = torch.tensor(u, dtype=torch.float64).to(torch.bfloat16)
+    out = ref.silu_mul(torch.cat((gt, ut)).view(1, -1), 4096).double().numpy()[0]
+    expect = brute.silu_mul_chain(g, u)
+    # fp32 silu in torch vs float64 silu: equal after bf16 rounding except at
+    # rounding ties of the intermediate; allow one bf16 ulp there.
+    assert np.mean(out == expect) > 0.995
+    assert np.all(np.abs(out - expect) <= brute.bf16_ulp(expect) + 1e-30)
+
+
+def test_logits_argmax_planted_and_ties():
+    v, k = 512, 64
+    rng = np.random.default_rng(9)
+    w = brute.f32_to_bf16_bits((rng.standard_normal((v, k)) * 0.02).astype(np.float32))
+    h = brute.f32_to_bf16_bits(rng.standard_normal((1, k)).astype(np.float32))
+    hot = brute.f32_to_bf16_bits((np.sign(brute.bf16_bits_to_f64(h[0])) * 0.5).astype(np.float32))
+    w[300] = hot
+    w[120] = hot  # identical maximal row at a lower index
+    wt, ht = from_bits(w), from_bits(h)[0]
+    assert ref.logits_argmax(ht, wt).item() == 120
+    assert ref.greedy_head_vector(ht, torch.ones(k, dtype=torch.bfloat16), wt, 1e-6).item() == 120
+    assert ref.bf16_logits_argmax(ht, wt).item() == 120
+    w[120] = brute.f32_to_bf16_bits(np.zeros(k, dtype=np.float32))
+    assert ref.logits_argmax(ht, from_bits(w)).item() == 300
+
+
+def test_logits_scores_are_fp32_accumulated():
+    """The cuTile head accumulates f32(W) * f32(h) in fp32 (cutile_logits.py:27):
+    the oracle's scores stay within the fp32 summation bound of float64."""
+    v, k = 256, 2560
+    rng = np.random.default_rng(10)
+    w = brute.f32_to_bf16_bits((rng.standard_normal((v, k)) * 0.02).astype(np.float32))
+    h = brute.f32_to_bf16_bits(rng.standard_normal((1, k)).astype(np.float32))
+    s = ref.logits_scores_fp32(from_bits(h)[0], from_bits(w)).double().numpy()
+    s64 = brute.linear64(h, w)[0]
+    assert np.all(np.abs(s - s64) <= brute.fp32_sum_bound(h, w)[0] + 1e-12)
+    # ... and are NOT rounded to bf16 (a bf16 head would fail this on random data)
+    assert np.any(np.abs(s - brute.round_bf16(s)) > 0)
+
+
+def test_mlp_epilogue_vector_composes_the_reference_steps():
+    """_semantic_mlp_epilogue_vector = residual + down(silu_mul(gate_up(rmsnorm(h))))."""
+    h_dim, inter = 64, 96
+    rng = np.random.default_rng(11)
+    hid = torch.tensor(rng.standard_normal(h_dim), dtype=torch.float32).to(torch.bfloat16)
+    ln = torch.tensor(1 + 0.1 * rng.standard_normal(h_dim), dtype=torch.float32).to(torch.bfloat16)
+    gu = torch.tensor(rng.standard_normal((2 * inter, h_dim)) * 0.05, dtype=torch.float32).to(torch.bfloat16)
+    dn = torch.tensor(rng.standard_normal((h_dim, inter)) * 0.05, dtype=torch.float32).to(torch.bfloat16)
+    out = ref.mlp_epilogue_vector(hid, ln, gu, inter, dn, 1e-6)
+    hf = hid.double()
+    normed = (hf / torch.sqrt((hf * hf).mean() + 1e-6) * ln.double())
+    g = gu.double() @ normed
+    act = torch.nn.functional.silu(g[:inter]) * g[inter:]
+    expect = hf + dn.double() @ act
+    assert torch.allclose(out.double(), expect, rtol=3e-2, atol=3e-2)
+    # the residual is really added: dropping it moves the result by |h|
+    assert (out.double() - (expect - hf)).abs().max() > 0.5
