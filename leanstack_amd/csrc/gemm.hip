@@ -11,9 +11,9 @@
 // Block tile 128 (weight rows) x 128 (tokens) x 64 (K), 4 wavefronts in a 2x2
 // arrangement, each owning 64x64 = 4x4 MFMA tiles; LDS is double buffered so
 // the global loads of stage s+1 are in flight while stage s is multiplied.
-// Workgroups are remapped so that each XCD walks a contiguous run of the
-// (weight block, token block) space: the token blocks sharing one weight
-// block then share that XCD's L2.
+// Workgroups are remapped so that each XCD walks a contiguous run of a
+// grouped (token block, weight block) order whose resident window shares its
+// weight and activation slices through the XCD's L2 (block_coords).
 //
 // Reference arithmetic replaced: F.linear at
 // src/leanstack/runtime/qwen_explicit.py:748, :819, :828, :830, :1202-1208 and
@@ -40,8 +40,15 @@ constexpr int kXTiles = kMbPerBlock * kKtPerStage;   // 16
 constexpr int kStageTiles = kWTiles + kXTiles;       // 32 x 1 KB
 constexpr int kLoadsPerThread = kStageTiles / kWaves;  // 8 (4 weight + 4 activation)
 
-__device__ __forceinline__ bf16x8_t zero_frag() {
-  return __builtin_bit_cast(bf16x8_t, u32x4_t{0u, 0u, 0u, 0u});
+// Activation chunk of row `row`; the load is unconditional so the main loop
+// has no branches that would split the accumulators' live ranges.  Rows past
+// M are clamped to row M-1 instead of zeroed: output row m depends on
+// activation row m only, and rows >= M are never stored, so the duplicate data
+// is harmless.  No mask means no use of the loaded value at load time, which
+// would force a vmcnt wait right after issue and expose the load latency.
+__device__ __forceinline__ bf16x8_t load_x_row(const __bf16* __restrict__ x, int ldx, int M, int row, int k) {
+  const int r = row < M ? row : M - 1;
+  return *reinterpret_cast<const bf16x8_t*>(x + (size_t)r * ldx + k);
 }
 
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
@@ -61,6 +68,27 @@ __device__ __forceinline__ float silu_mul_bf16(float g_acc, float u_acc) {
   const float u = bf16_round(u_acc);
   const float s = bf16_round(g / (1.0f + expf(-g)));
   return bf16_round(s * u);
+}
+
+// Block order.  Workgroup b runs on XCD b % 8 (round-robin dispatch), so each
+// XCD gets a contiguous run of the logical order; inside it, tiles go in
+// groups of kGroupM token blocks, all weight blocks of a group before the next
+// group, token-block fastest.  The ~32 workgroups resident on one XCD at a
+// time then cover about kGroupM token blocks x 32/kGroupM weight blocks, so
+// their weight and activation slices are shared through that XCD's L2
+// instead of the whole activation matrix being re-streamed per weight block.
+constexpr int kGroupM = 8;
+
+__device__ __forceinline__ void block_coords(int n_blocks, int m_blocks, int& nb, int& mb) {
+  const int total = n_blocks * m_blocks;
+  int logical = blockIdx.x;
+  if (total % 8 == 0) logical = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
+  const int group = logical / (kGroupM * n_blocks);
+  const int first_m = group * kGroupM;
+  const int group_m = min(m_blocks - first_m, kGroupM);
+  const int in_group = logical - group * kGroupM * n_blocks;
+  mb = first_m + in_group % group_m;
+  nb = in_group / group_m;
 }
 
 struct StageRegs {
@@ -84,7 +112,7 @@ __device__ __forceinline__ void load_stage(StageRegs& r, const bf16x8_t* __restr
     const int t = wave * 4 + j;
     const int row = m_base + (t / kKtPerStage) * 16 + (lane & 15);
     const int k = (kt0 + t % kKtPerStage) * kTileK + 8 * (lane >> 4);
-    r.v[4 + j] = row < M ? *reinterpret_cast<const bf16x8_t*>(x + (size_t)row * ldx + k) : zero_frag();
+    r.v[4 + j] = load_x_row(x, ldx, M, row, k);
   }
 }
 
@@ -103,13 +131,8 @@ __global__ __launch_bounds__(kThreads) void gemm_linear_kernel(const bf16x8_t* _
                                                                int M, int KT, int n_blocks, int m_blocks) {
   __shared__ bf16x8_t lds[2][kStageTiles][64];
 
-  // XCD-aware remap: workgroup b runs on XCD b % 8; give each XCD a
-  // contiguous run of logical tiles (weight-block major).
-  const int total = n_blocks * m_blocks;
-  int logical = blockIdx.x;
-  if (total % 8 == 0) logical = (blockIdx.x % 8) * (total / 8) + blockIdx.x / 8;
-  const int nb = logical / m_blocks;
-  const int mb = logical % m_blocks;
+  int nb, mb;
+  block_coords(n_blocks, m_blocks, nb, mb);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -130,10 +153,7 @@ __global__ __launch_bounds__(kThreads) void gemm_linear_kernel(const bf16x8_t* _
   store_stage(lds[0], regs, wave, lane);
   __syncthreads();
 
-  for (int s = 0; s < stages; ++s) {
-    const int cur = s & 1;
-    const bool more = s + 1 < stages;
-    if (more) load_stage(regs, w, x, ldx, M, KT, rb_base, m_base, (s + 1) * kKtPerStage, wave, lane);
+  auto compute = [&](int cur) {
 #pragma unroll
     for (int kk = 0; kk < kKtPerStage; ++kk) {
       bf16x8_t wf[4], xf[4];
@@ -146,9 +166,15 @@ __global__ __launch_bounds__(kThreads) void gemm_linear_kernel(const bf16x8_t* _
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(wf[a], xf[b], acc[a][b]);
     }
-    if (more) store_stage(lds[cur ^ 1], regs, wave, lane);
+  };
+  for (int s = 0; s + 1 < stages; ++s) {
+    load_stage(regs, w, x, ldx, M, KT, rb_base, m_base, (s + 1) * kKtPerStage, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s & 1);
+    store_stage(lds[(s + 1) & 1], regs, wave, lane);
     __syncthreads();
   }
+  compute((stages - 1) & 1);
 
   // Lane (g, c) of tile (a, b) holds rows 4g..4g+3 of weight row-block a
   // for token c of token block b.
@@ -188,6 +214,255 @@ __global__ __launch_bounds__(kThreads) void gemm_linear_kernel(const bf16x8_t* _
   }
 }
 
+// ---------------------------------------------------------------------------
+// Large-tile variant: 256 (weight rows) x 256 (tokens) x 64 (K) blocks, four
+// waves each owning a 128 x 128 tile of v_mfma_f32_32x32x16_bf16 (the full-
+// rate MFMA on gfx950; the 16x16x32 form issues at about half its rate).  A
+// 128 x 128 wave tile reads 8 KB of operands from LDS per 64 MFMAs, half the
+// LDS bandwidth at peak MFMA rate, where the 64 x 64 tiles above need all of
+// it.  Accumulators (256 per lane) live in the accumulation registers.
+//
+// Weight operand: a 32-row x 16-K A fragment is assembled from two packed
+// 16 x 32 tiles by lane remapping (rows 0-15 from tile 2a, 16-31 from 2a+1),
+// so the weights still arrive in LDS by a linear 1 KB copy per tile.  For the
+// gate/up layout that pairing puts gate rows 0-15 and up rows 16-31 of the
+// same 16 intermediate outputs in the same lane (accumulator j and j + 8).
+// Activation operand: 32 tokens x 16 K fragments in B-operand lane order,
+// with an XOR swizzle on the token slot so that both the coalesced global
+// reads (8 lanes per 128-byte row) and the fragment reads hit 16 distinct
+// bank groups per 16-lane pass.
+namespace big {
+
+constexpr int BN = 256, BM = 256, BK = 64;
+constexpr int kThreads = 256;
+constexpr int kWBytes = BN * BK * 2;                // 32 KB of weight tiles per stage
+constexpr int kStageBytes = kWBytes + BM * BK * 2;  // + 32 KB of activation fragments
+constexpr int kChunks = 8;                          // 16-byte chunks per thread per half-stage
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16_t mfma32(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// LDS byte offset of activation chunk (token m of the block, 8-wide K group k8 of the stage).
+__device__ __forceinline__ int x_lds_off(int m, int k8) {
+  return kWBytes + ((m >> 5) * 4 + (k8 >> 1)) * 1024 + ((((m & 31) ^ (2 * k8)) + 32 * (k8 & 1)) << 4);
+}
+
+struct Regs {
+  bf16x8_t w[kChunks];
+  bf16x8_t x[kChunks];
+};
+
+__device__ __forceinline__ void load_w(Regs& r, const bf16x8_t* __restrict__ w, int KT, int rb0, int s, int tid) {
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int u = c * kThreads + tid;
+    const int tile = u >> 6;  // 32 tiles: (row-block, k-tile) = (tile / 2, tile % 2)
+    r.w[c] = w[((size_t)(rb0 + (tile >> 1)) * KT + 2 * s + (tile & 1)) * 64 + (u & 63)];
+  }
+}
+
+__device__ __forceinline__ void load_x(Regs& r, const __bf16* __restrict__ x, int ldx, int M, int m0, int s,
+                                       int tid) {
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int u = c * kThreads + tid;
+    r.x[c] = load_x_row(x, ldx, M, m0 + (u >> 3), s * BK + (u & 7) * 8);
+  }
+}
+
+__device__ __forceinline__ void store_stage(unsigned char* buf, const Regs& r, int tid) {
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int u = c * kThreads + tid;
+    *reinterpret_cast<bf16x8_t*>(buf + u * 16) = r.w[c];
+  }
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int u = c * kThreads + tid;
+    *reinterpret_cast<bf16x8_t*>(buf + x_lds_off(u >> 3, u & 7)) = r.x[c];
+  }
+}
+
+// Instruction-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm256_kernel(const bf16x8_t* __restrict__ w,
+                                                              const __bf16* __restrict__ x, int ldx,
+                                                              __bf16* __restrict__ y, int ldy,
+                                                              const __bf16* __restrict__ residual, int ldr, int M,
+                                                              int KT, int n_blocks, int m_blocks) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kStageBytes];
+
+  int nb, mb;
+  block_coords(n_blocks, m_blocks, nb, mb);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int rb0 = nb * (BN / kTileRows);
+  const int m0 = mb * BM;
+
+  // Per-lane fragment offsets inside a stage.  Weight A fragment for n-tile
+  // `an` (32 rows) and 16-K step q: rows from tiles 2an / 2an+1.
+  const int li = lane & 31;
+  const int kg = lane >> 5;
+  const int w_lane = (li >> 4) * 2048 + kg * 256 + (li & 15) * 16;
+  int x_lane[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) x_lane[q] = kWBytes + q * 1024 + ((((li) ^ (4 * q + 2 * kg)) + 32 * kg) << 4);
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+
+  // Fragments of one 16-K step: four 32-row weight tiles, four 32-token activation tiles.
+  auto read_frags = [&](bf16x8_t* fa, bf16x8_t* fb, const unsigned char* buf, int q) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      fa[a] = *reinterpret_cast<const bf16x8_t*>(buf + (wn * 4 + a) * 4096 + q * 512 + w_lane);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) fb[b] = *reinterpret_cast<const bf16x8_t*>(buf + (wm * 4 + b) * 4096 + x_lane[q]);
+  };
+  auto mfma_step = [&](const bf16x8_t* fa, const bf16x8_t* fb) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(fa[a], fb[b], acc[a][b]);
+  };
+
+  // Software pipeline over 64-K stages with two LDS buffers.  While the MFMAs
+  // of stage s run on buffer s&1, the same instruction stream (i) reads the
+  // fragments of the next 16-K step into the idle register set, (ii) writes
+  // stage s+1 from registers into buffer (s+1)&1 and (iii) issues the global
+  // loads of stage s+2.  One barrier per stage, before the last 16-K step,
+  // publishes buffer (s+1)&1 and retires every read of buffer s&1.  Stage
+  // indices past the end are clamped: the redundant loads stay in bounds and
+  // the data they stage is never multiplied.
+  const int stages = KT / 2;
+  Regs regs;
+  load_w(regs, w, KT, rb0, 0, tid);
+  load_x(regs, x, ldx, M, m0, 0, tid);
+  store_stage(lds, regs, tid);
+  const int s1 = min(1, stages - 1);
+  load_w(regs, w, KT, rb0, s1, tid);
+  load_x(regs, x, ldx, M, m0, s1, tid);
+  __syncthreads();
+
+  bf16x8_t fa0[4], fb0[4], fa1[4], fb1[4];
+  read_frags(fa0, fb0, lds, 0);
+  for (int s = 0; s < stages; ++s) {
+    const unsigned char* cur = lds + (s & 1) * kStageBytes;
+    unsigned char* nxt = lds + ((s + 1) & 1) * kStageBytes;
+    const int ls = min(s + 2, stages - 1);
+
+    read_frags(fa1, fb1, cur, 1);
+    mfma_step(fa0, fb0);
+    store_stage(nxt, regs, tid);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 2, 0);
+    }
+
+    read_frags(fa0, fb0, cur, 2);
+    load_w(regs, w, KT, rb0, ls, tid);
+    mfma_step(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+
+    read_frags(fa1, fb1, cur, 3);
+    load_x(regs, x, ldx, M, m0, ls, tid);
+    mfma_step(fa0, fb0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+
+    __syncthreads();
+    read_frags(fa0, fb0, nxt, 0);
+    mfma_step(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+  }
+
+  // Lane l of tile (a, b) holds D[8*(j/4) + 4*(l/32) + j%4][l%32], j = 0..15.
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int m = m0 + (wm * 4 + b) * 32 + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int an = nb * 8 + wn * 4 + a;  // global 32-row tile index
+      if constexpr (EPI == static_cast<int>(Epilogue::kSiluMul)) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int n = an * 16 + 8 * jj + 4 * kg;  // intermediate column
+          unsigned short o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = bf16_bits(silu_mul_bf16(acc[a][b][4 * jj + e], acc[a][b][4 * jj + 8 + e]));
+          *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
+              u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+        }
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int n = an * 32 + 8 * jj + 4 * kg;
+          unsigned short o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = bf16_round(acc[a][b][4 * jj + e]);
+            if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd))
+              v = static_cast<float>(residual[(size_t)m * ldr + n + e]) + v;
+            o[e] = bf16_bits(v);
+          }
+          *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
+              u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
+                  const void* residual, int ldr, hipStream_t stream) {
+  const int n_blocks = N / BN;
+  const int m_blocks = (M + BM - 1) / BM;
+  gemm256_kernel<EPI><<<dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream>>>(
+      static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
+      static_cast<const __bf16*>(residual), ldr, M, K / kTileK, n_blocks, m_blocks);
+  return hipGetLastError();
+}
+
+}  // namespace big
+
 template <int EPI>
 hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
                       const void* residual, int ldr, hipStream_t stream) {
@@ -203,6 +478,17 @@ hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx
 
 hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
                               Epilogue epi, const void* residual, int ldr, hipStream_t stream) {
+  if (M > kGemmBM && N % big::BN == 0 && K % big::BK == 0) {
+    switch (epi) {
+      case Epilogue::kSiluMul:
+        return big::launch<1>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+      case Epilogue::kResidualAdd:
+        return big::launch<2>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+      case Epilogue::kNone:
+      default:
+        return big::launch<0>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+    }
+  }
   switch (epi) {
     case Epilogue::kSiluMul:
       return launch_cfg<1>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);

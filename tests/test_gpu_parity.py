@@ -191,3 +191,22 @@ def test_rejects_bad_shapes_before_launch(gpu):
         kernels.linear(activations(1, 64, seed=2).to(dev), pw, epilogue=_lib.EPI_SILU_MUL)
     with pytest.raises(ValueError):
         kernels.lm_head_argmax(activations(17, 64, seed=2).to(dev), pw)
+
+
+@pytest.mark.parametrize("name", sorted(PROJ) + ["gate_up_proj"])
+def test_prefill_m2048_full_shapes(gpu, name):
+    """M=2048 at every projection shape (the large-tile MFMA kernel), against the oracle."""
+    m = 2048
+    if name == "gate_up_proj":
+        n, k = 2 * G.intermediate_size, G.hidden_size
+        w = weight(n, k, seed=81)
+        x = activations(m, k, seed=810)
+        y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
+        expect = ref.silu_mul(ref.linear(x, w), G.intermediate_size)
+    else:
+        n, k = PROJ[name]
+        w = weight(n, k, seed=82)
+        x = activations(m, k, seed=820)
+        y = _gpu_linear(x, w)
+        expect = ref.linear(x, w)
+    assert_parity(y, expect, f"{name} prefill M=2048")
