@@ -463,6 +463,252 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 
 }  // namespace big
 
+// Weights-direct variant of the 256x256x64 kernel.  Each wave loads its own
+// weight fragments from global memory straight into registers: a packed 1 KB
+// tile already is MFMA operand data in lane order, so a 32-row A fragment is
+// two 512-byte contiguous runs and needs no LDS staging.  Only the
+// activations go through LDS.  Per stage and CU this moves 96 KB through LDS
+// (32 KB activation writes, 64 KB fragment reads) instead of 192 KB; the two
+// waves that share a weight-row half fetch the same lines, the second mostly
+// from L1.  Weight fragments are prefetched one stage ahead into the idle one
+// of two register sets; the stage loop is unrolled by two so the sets swap
+// roles without copies, which requires an even number of stages.
+namespace wdx {
+
+constexpr int BN = 256, BM = 256, BK = 64;
+constexpr int kThreads = 256;
+constexpr int kXStageBytes = BM * BK * 2;  // 32 KB of activation fragments per stage
+constexpr int kXChunks = 8;                // 16-byte activation chunks per thread per stage
+
+using big::f32x16_t;
+using big::mfma32;
+using big::kSchedMfma;
+using big::kSchedVmemRead;
+using big::kSchedDsRead;
+using big::kSchedDsWrite;
+
+__device__ __forceinline__ int x_lds_off(int m, int k8) {
+  return ((m >> 5) * 4 + (k8 >> 1)) * 1024 + ((((m & 31) ^ (2 * k8)) + 32 * (k8 & 1)) << 4);
+}
+
+struct XRegs {
+  bf16x8_t v[kXChunks];
+};
+
+struct WFrags {
+  bf16x8_t v[4][4];  // [16-K step q][32-row tile a]
+};
+
+// A fragment (32 rows x 16 K) of tile a, step q: lane (li, kg) takes row li of
+// the two 16-row packed tiles 2a, 2a+1 and K chunk 2(q&1)+kg of k-tile q/2.
+__device__ __forceinline__ void load_w(WFrags& f, const bf16x8_t* __restrict__ wl, int KT, int s) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) f.v[q][a] = wl[((size_t)(2 * a) * KT + 2 * s + (q >> 1)) * 64 + (q & 1) * 32];
+}
+
+__device__ __forceinline__ void load_x(XRegs& r, const __bf16* __restrict__ x, int ldx, int M, int m0, int s,
+                                       int tid) {
+#pragma unroll
+  for (int c = 0; c < kXChunks; ++c) {
+    const int u = c * kThreads + tid;
+    r.v[c] = load_x_row(x, ldx, M, m0 + (u >> 3), s * BK + (u & 7) * 8);
+  }
+}
+
+__device__ __forceinline__ void store_x(unsigned char* buf, const XRegs& r, int tid) {
+#pragma unroll
+  for (int c = 0; c < kXChunks; ++c) {
+    const int u = c * kThreads + tid;
+    *reinterpret_cast<bf16x8_t*>(buf + x_lds_off(u >> 3, u & 7)) = r.v[c];
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(const bf16x8_t* __restrict__ w,
+                                                               const __bf16* __restrict__ x, int ldx,
+                                                               __bf16* __restrict__ y, int ldy,
+                                                               const __bf16* __restrict__ residual, int ldr, int M,
+                                                               int KT, int n_blocks, int m_blocks) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXStageBytes];
+
+  int nb, mb;
+  block_coords(n_blocks, m_blocks, nb, mb);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int m0 = mb * BM;
+  const int li = lane & 31;
+  const int kg = lane >> 5;
+
+  // This lane's element of weight fragment (a=0, q=0, stage 0).
+  const bf16x8_t* wl = w + ((size_t)(nb * (BN / kTileRows) + wn * 8 + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
+  int x_lane[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) x_lane[q] = wm * 4 * 4096 + q * 1024 + (((li ^ (4 * q + 2 * kg)) + 32 * kg) << 4);
+
+  f32x16_t acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+
+  auto read_b = [&](bf16x8_t* fb, const unsigned char* buf, int q) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) fb[b] = *reinterpret_cast<const bf16x8_t*>(buf + b * 4096 + x_lane[q]);
+  };
+  auto mfma_step = [&](const bf16x8_t* fa, const bf16x8_t* fb) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(fa[a], fb[b], acc[a][b]);
+  };
+
+  const int stages = KT / 2;
+  XRegs xr;
+  WFrags wf0, wf1;
+  bf16x8_t fb0[4], fb1[4];
+
+  // One stage on LDS buffer s&1 with weight fragments wc, prefetching stage
+  // s+1's weights into wn_ and stage s+2's activations.  The barrier before
+  // the last 16-K step publishes buffer (s+1)&1 (written in step 1) and
+  // retires every read of buffer s&1.  Stage indices past the end are
+  // clamped: the redundant loads stay in bounds and are never multiplied.
+  auto stage = [&](int s, const WFrags& wc, WFrags& wn_) {
+    const unsigned char* cur = lds + (s & 1) * kXStageBytes;
+    unsigned char* nxt = lds + ((s + 1) & 1) * kXStageBytes;
+    const int sw = min(s + 1, stages - 1);
+    const int sx = min(s + 2, stages - 1);
+
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(fb1, cur, 1);
+    load_w(wn_, wl, KT, sw);
+    mfma_step(wc.v[0], fb0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(fb0, cur, 2);
+    store_x(nxt, xr, tid);
+    mfma_step(wc.v[1], fb1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(fb1, cur, 3);
+    load_x(xr, x, ldx, M, m0, sx, tid);
+    mfma_step(wc.v[2], fb0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+
+    __syncthreads();
+    read_b(fb0, nxt, 0);
+    mfma_step(wc.v[3], fb1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 12, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  load_x(xr, x, ldx, M, m0, 0, tid);
+  load_w(wf0, wl, KT, 0);
+  store_x(lds, xr, tid);
+  load_x(xr, x, ldx, M, m0, min(1, stages - 1), tid);
+  __syncthreads();
+  read_b(fb0, lds, 0);
+  for (int s = 0; s < stages; s += 2) {
+    stage(s, wf0, wf1);
+    stage(s + 1, wf1, wf0);
+  }
+
+  // Lane l of tile (a, b) holds D[8*(j/4) + 4*(l/32) + j%4][l%32], j = 0..15.
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int m = m0 + (wm * 4 + b) * 32 + li;
+    if (m >= M) continue;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int an = nb * 8 + wn * 4 + a;  // global 32-row tile index
+      if constexpr (EPI == static_cast<int>(Epilogue::kSiluMul)) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const int n = an * 16 + 8 * jj + 4 * kg;  // intermediate column
+          unsigned short o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = bf16_bits(silu_mul_bf16(acc[a][b][4 * jj + e], acc[a][b][4 * jj + 8 + e]));
+          *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
+              u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+        }
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int n = an * 32 + 8 * jj + 4 * kg;
+          unsigned short o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = bf16_round(acc[a][b][4 * jj + e]);
+            if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd))
+              v = static_cast<float>(residual[(size_t)m * ldr + n + e]) + v;
+            o[e] = bf16_bits(v);
+          }
+          *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
+              u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
+                  const void* residual, int ldr, hipStream_t stream) {
+  const int n_blocks = N / BN;
+  const int m_blocks = (M + BM - 1) / BM;
+  gemm_wdx_kernel<EPI><<<dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream>>>(
+      static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
+      static_cast<const __bf16*>(residual), ldr, M, K / kTileK, n_blocks, m_blocks);
+  return hipGetLastError();
+}
+
+}  // namespace wdx
+
 template <int EPI>
 hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
                       const void* residual, int ldr, hipStream_t stream) {
@@ -478,6 +724,17 @@ hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx
 
 hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
                               Epilogue epi, const void* residual, int ldr, hipStream_t stream) {
+  if (M > kGemmBM && N % wdx::BN == 0 && K % (2 * wdx::BK) == 0) {
+    switch (epi) {
+      case Epilogue::kSiluMul:
+        return wdx::launch<1>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+      case Epilogue::kResidualAdd:
+        return wdx::launch<2>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+      case Epilogue::kNone:
+      default:
+        return wdx::launch<0>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+    }
+  }
   if (M > kGemmBM && N % big::BN == 0 && K % big::BK == 0) {
     switch (epi) {
       case Epilogue::kSiluMul:
