@@ -84,9 +84,11 @@ const char* lsk_last_error(void);
 size_t lsk_packed_bytes(int layout_id, int N, int K);
 
 /* Device workspace that `op` needs for M rows of an [N, K] weight.  The
- * caller allocates it once and passes it to every call of that op.
- * Replaces the tile_scores / tile_argmax scratch that
- * src/leanstack/runtime/cutile_logits.py:56-58 allocates per call. */
+ * caller allocates it once and passes it to every call of that op.  For
+ * LSK_OP_LM_HEAD_ARGMAX it is required; it replaces the tile_scores /
+ * tile_argmax scratch that src/leanstack/runtime/cutile_logits.py:56-58
+ * allocates per call.  For LSK_OP_LINEAR it is optional and sized for the
+ * current device's CU count (0 when the shape does not use one). */
 size_t lsk_workspace_bytes(int op, int M, int N, int K);
 
 /* Host-side packer: re-tile row-major W[N][K] bf16 (`w_rowmajor_host`) into
@@ -111,6 +113,13 @@ int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* 
  *   M          >= 1.  M <= 16 runs the decode/verify kernel (weights streamed
  *              once, activations padded to the 16 MFMA columns); larger M
  *              runs the prefill MFMA GEMM.
+ *   workspace  NULL, or (prefill) lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K)
+ *              bytes, 256-byte aligned, zero-filled before its first use.
+ *              With it, the prefill GEMM splits the K range of its output
+ *              blocks over all CUs (stream-K) and adds the fp32 partials in a
+ *              fixed order; without it, one workgroup per output block.  Calls
+ *              leave it as they found it (see lsk_linear_error); calls that
+ *              share one must be stream-ordered.  Ignored for M <= 16.
  * Replaces torch.mv / F.linear at src/leanstack/runtime/qwen_explicit.py:748,
  * :787, :819, :828-830, :913, :942-948, :1202-1208. */
 int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K,
@@ -191,6 +200,13 @@ int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws
  * of every launch since the last call completed; nonzero = a bounded wait
  * gave up (outputs of that launch are invalid). */
 int lsk_stack_error(void* workspace, int* error_out);
+
+/* Read (synchronously) and clear the error word of a prefill workspace:
+ * 0 = every wait of every stream-K launch since the last call completed;
+ * nonzero = a bounded wait for another workgroup's partial gave up (outputs
+ * of that launch are invalid).  No counterpart in the reference, whose
+ * library GEMMs have no cross-workgroup waits. */
+int lsk_linear_error(void* workspace, int* error_out);
 
 #ifdef __cplusplus
 }

@@ -36,6 +36,9 @@ ERR_LAYOUT = -2
 ERR_HIP = -3
 ERR_WORKSPACE = -4
 
+# Largest M served by the decode/verify kernel (kDecodeMaxM in the library).
+DECODE_MAX_M = 16
+
 _c_int = ctypes.c_int
 _c_size = ctypes.c_size_t
 _c_void = ctypes.c_void_p
@@ -85,6 +88,7 @@ _SIGNATURES.update({
     "lsk_stack_prepare": (_c_int, [ctypes.POINTER(Projection), _c_int, _c_int, _c_void, _c_size]),
     "lsk_stack_run": (_c_int, [_c_void, _c_int, _c_void, _c_size, _c_void]),
     "lsk_stack_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
+    "lsk_linear_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
 })
 
 _lock = threading.Lock()

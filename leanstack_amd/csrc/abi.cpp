@@ -78,6 +78,20 @@ inline size_t packed_unit(int K, int pr, int k8) {
 
 }  // namespace
 
+// Synchronously read and clear word `index` of a workspace.
+int read_clear_error_word(void* workspace, int index, int* error_out) {
+  if (workspace == nullptr || error_out == nullptr) return fail(LSK_ERR_INVALID, "null argument");
+  unsigned word = 0;
+  auto* err_word = static_cast<unsigned*>(workspace) + index;
+  hipError_t err = hipMemcpy(&word, err_word, sizeof(word), hipMemcpyDeviceToHost);
+  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(workspace error word)");
+  const unsigned zero = 0;
+  err = hipMemcpy(err_word, &zero, sizeof(zero), hipMemcpyHostToDevice);
+  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(clear workspace error word)");
+  *error_out = (int)word;
+  return LSK_OK;
+}
+
 extern "C" {
 
 int lsk_abi_version(void) { return LSK_ABI_VERSION; }
@@ -90,7 +104,14 @@ size_t lsk_packed_bytes(int layout_id, int N, int K) {
 }
 
 size_t lsk_workspace_bytes(int op, int M, int N, int K) {
-  if (op == LSK_OP_LINEAR) return 0;
+  if (op == LSK_OP_LINEAR) {
+    if (M <= lsk::kDecodeMaxM || N <= 0 || K <= 0) return 0;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) return 0;
+    hipError_t err;
+    const size_t bytes = lsk::gemm_workspace_bytes(device, M, N, K, &err);
+    return err == hipSuccess ? bytes : 0;
+  }
   if (op == LSK_OP_LM_HEAD_ARGMAX) {
     if (M < 1 || M > lsk::kDecodeMaxM || N <= 0 || K <= 0 || N % (2 * lsk::kTileRows) != 0) return 0;
     return (size_t)M * (size_t)lsk::lm_head_partials(N) * sizeof(lsk::ArgmaxPartial);
@@ -129,8 +150,6 @@ int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* 
 int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx, void* y,
                     int ldy, int epilogue, const void* residual, int ldr, void* workspace, size_t ws_bytes,
                     void* hip_stream) {
-  (void)workspace;
-  (void)ws_bytes;
   g_last_error.clear();
   if (int st = check_shape(layout_id, N, K)) return st;
   if (epilogue != LSK_EPI_NONE && epilogue != LSK_EPI_SILU_MUL && epilogue != LSK_EPI_RESIDUAL_ADD)
@@ -158,7 +177,17 @@ int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const voi
   if (M <= lsk::kDecodeMaxM) {
     err = lsk::launch_decode_linear(w_packed, N, K, x, M, ldx, y, ldy, epi, residual, ldr, stream);
   } else if (gemm_shape) {
-    err = lsk::launch_gemm_linear(w_packed, N, K, x, M, ldx, y, ldy, epi, residual, ldr, stream);
+    if (workspace != nullptr) {
+      int device = 0;
+      err = hipGetDevice(&device);
+      if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+      const size_t need = lsk::gemm_workspace_bytes(device, M, N, K, &err);
+      if (err != hipSuccess) return hip_fail(err, "prefill workspace size");
+      if (ws_bytes < need || !aligned(workspace, 256))
+        return fail(LSK_ERR_WORKSPACE, "prefill workspace needs %zu bytes, 256-byte aligned (got %zu)", need, ws_bytes);
+    }
+    err = lsk::launch_gemm_linear(w_packed, N, K, x, M, ldx, y, ldy, epi, residual, ldr, workspace, ws_bytes,
+                                  stream);
   } else {
     // Shapes off the GEMM tile grid: decode kernel over 16-row slices.
     err = hipSuccess;
@@ -325,16 +354,12 @@ int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws
 
 int lsk_stack_error(void* workspace, int* error_out) {
   g_last_error.clear();
-  if (workspace == nullptr || error_out == nullptr) return fail(LSK_ERR_INVALID, "null argument");
-  unsigned word = 0;
-  auto* err_word = static_cast<unsigned*>(workspace) + lsk::kStackWsError;
-  hipError_t err = hipMemcpy(&word, err_word, sizeof(word), hipMemcpyDeviceToHost);
-  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(stack error word)");
-  const unsigned zero = 0;
-  err = hipMemcpy(err_word, &zero, sizeof(zero), hipMemcpyHostToDevice);
-  if (err != hipSuccess) return hip_fail(err, "hipMemcpy(clear stack error word)");
-  *error_out = (int)word;
-  return LSK_OK;
+  return read_clear_error_word(workspace, lsk::kStackWsError, error_out);
+}
+
+int lsk_linear_error(void* workspace, int* error_out) {
+  g_last_error.clear();
+  return read_clear_error_word(workspace, 0, error_out);
 }
 
 }  // extern "C"

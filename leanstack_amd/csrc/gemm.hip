@@ -21,6 +21,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+#include <vector>
+
 #include "lsk_internal.h"
 
 namespace lsk {
@@ -525,18 +528,33 @@ __device__ __forceinline__ void store_x(unsigned char* buf, const XRegs& r, int 
   }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(const bf16x8_t* __restrict__ w,
-                                                               const __bf16* __restrict__ x, int ldx,
-                                                               __bf16* __restrict__ y, int ldy,
-                                                               const __bf16* __restrict__ residual, int ldr, int M,
-                                                               int KT, int n_blocks, int m_blocks) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXStageBytes];
+struct Args {
+  const bf16x8_t* w;
+  const __bf16* x;
+  __bf16* y;
+  const __bf16* residual;
+  int ldx, ldy, ldr, M, KT, n_blocks, m_blocks;
+};
 
-  int nb, mb;
-  block_coords(n_blocks, m_blocks, nb, mb);
-
-  const int tid = threadIdx.x;
+// acc[a][b] += W rows of 32-row tiles (wn*4 + a) x tokens of 32-token tiles
+// (wm*4 + b) over stages [s0, s1) (s1 - s0 even) of block (nb, mb).
+//
+// Software pipeline over 64-K stages with two LDS activation buffers.  While
+// the MFMAs of stage s run on buffer s&1 with weight fragments wc, the same
+// instruction stream reads the activation fragments of the next 16-K step,
+// loads stage s+1's weight fragments into the idle register set, writes
+// stage s+1's activations (loaded one stage earlier) into buffer (s+1)&1 and
+// issues the activation loads of stage s+2.  The barrier before the last
+// 16-K step publishes buffer (s+1)&1 and retires every read of buffer s&1.
+// Stage indices past s1 are clamped: those loads stay in bounds and the data
+// they stage is never multiplied.
+__device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, unsigned char* lds, int nb, int mb,
+                                         int s0, int s1) {
+  // Opaque per call: keeps the per-lane offsets below from being hoisted out
+  // of a caller's loop over blocks, where they would stay live (and spill)
+  // across the epilogues.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wn = wave & 1;
@@ -544,20 +562,13 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(const bf16x8_t* _
   const int m0 = mb * BM;
   const int li = lane & 31;
   const int kg = lane >> 5;
+  const int KT = g.KT;
 
-  // This lane's element of weight fragment (a=0, q=0, stage 0).
-  const bf16x8_t* wl = w + ((size_t)(nb * (BN / kTileRows) + wn * 8 + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
+  // This lane's element of weight fragment (a=0, q=0) at stage 0.
+  const bf16x8_t* wl = g.w + ((size_t)(nb * (BN / kTileRows) + wn * 8 + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
   int x_lane[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) x_lane[q] = wm * 4 * 4096 + q * 1024 + (((li ^ (4 * q + 2 * kg)) + 32 * kg) << 4);
-
-  f32x16_t acc[4][4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
 
   auto read_b = [&](bf16x8_t* fb, const unsigned char* buf, int q) {
 #pragma unroll
@@ -570,21 +581,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(const bf16x8_t* _
       for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(fa[a], fb[b], acc[a][b]);
   };
 
-  const int stages = KT / 2;
   XRegs xr;
   WFrags wf0, wf1;
   bf16x8_t fb0[4], fb1[4];
 
-  // One stage on LDS buffer s&1 with weight fragments wc, prefetching stage
-  // s+1's weights into wn_ and stage s+2's activations.  The barrier before
-  // the last 16-K step publishes buffer (s+1)&1 (written in step 1) and
-  // retires every read of buffer s&1.  Stage indices past the end are
-  // clamped: the redundant loads stay in bounds and are never multiplied.
   auto stage = [&](int s, const WFrags& wc, WFrags& wn_) {
     const unsigned char* cur = lds + (s & 1) * kXStageBytes;
     unsigned char* nxt = lds + ((s + 1) & 1) * kXStageBytes;
-    const int sw = min(s + 1, stages - 1);
-    const int sx = min(s + 2, stages - 1);
+    const int sw = min(s + 1, s1 - 1);
+    const int sx = min(s + 2, s1 - 1);
 
     __builtin_amdgcn_sched_barrier(0);
     read_b(fb1, cur, 1);
@@ -620,7 +625,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(const bf16x8_t* _
 
     __builtin_amdgcn_sched_barrier(0);
     read_b(fb1, cur, 3);
-    load_x(xr, x, ldx, M, m0, sx, tid);
+    load_x(xr, g.x, g.ldx, g.M, m0, sx, tid);
     mfma_step(wc.v[2], fb0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -647,63 +652,277 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(const bf16x8_t* _
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  load_x(xr, x, ldx, M, m0, 0, tid);
-  load_w(wf0, wl, KT, 0);
-  store_x(lds, xr, tid);
-  load_x(xr, x, ldx, M, m0, min(1, stages - 1), tid);
+  // Every wave is past its last read of either buffer (a previous block's
+  // stages) before the prologue overwrites buffer s0&1.
   __syncthreads();
-  read_b(fb0, lds, 0);
-  for (int s = 0; s < stages; s += 2) {
+  load_x(xr, g.x, g.ldx, g.M, m0, s0, tid);
+  load_w(wf0, wl, KT, s0);
+  store_x(lds + (s0 & 1) * kXStageBytes, xr, tid);
+  load_x(xr, g.x, g.ldx, g.M, m0, min(s0 + 1, s1 - 1), tid);
+  __syncthreads();
+  read_b(fb0, lds + (s0 & 1) * kXStageBytes, 0);
+  for (int s = s0; s < s1; s += 2) {
     stage(s, wf0, wf1);
     stage(s + 1, wf1, wf0);
   }
+}
 
-  // Lane l of tile (a, b) holds D[8*(j/4) + 4*(l/32) + j%4][l%32], j = 0..15.
+// Epilogue of this lane's 32x32 tile (a, b) of block (nb, mb).  src(p)
+// returns elements 2p, 2p+1 of the lane's 16 fp32 results of the tile.
+// Lane l of tile (a, b) holds D[8*(j/4) + 4*(l/32) + j%4][l%32], j = 0..15.
+template <int EPI, typename Src>
+__device__ __forceinline__ void store_one_tile(Src src, const Args& g, int nb, int mb, int a, int b) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+  const int li = lane & 31;
+  const int kg = lane >> 5;
+  const int m = mb * BM + (wm * 4 + b) * 32 + li;
+  if (m >= g.M) return;
+  const int an = nb * 8 + wn * 4 + a;  // global 32-row tile index
+  if constexpr (EPI == static_cast<int>(Epilogue::kSiluMul)) {
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const int m = m0 + (wm * 4 + b) * 32 + li;
-    if (m >= M) continue;
+    for (int jj = 0; jj < 2; ++jj) {
+      const int n = an * 16 + 8 * jj + 4 * kg;  // intermediate column
+      const float2 g0 = src(2 * jj), g1 = src(2 * jj + 1);
+      const float2 u0 = src(2 * jj + 4), u1 = src(2 * jj + 5);
+      const unsigned short o0 = bf16_bits(silu_mul_bf16(g0.x, u0.x));
+      const unsigned short o1 = bf16_bits(silu_mul_bf16(g0.y, u0.y));
+      const unsigned short o2 = bf16_bits(silu_mul_bf16(g1.x, u1.x));
+      const unsigned short o3 = bf16_bits(silu_mul_bf16(g1.y, u1.y));
+      *reinterpret_cast<u32x2_t*>(g.y + (size_t)m * g.ldy + n) =
+          u32x2_t{o0 | ((unsigned)o1 << 16), o2 | ((unsigned)o3 << 16)};
+    }
+  } else {
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int an = nb * 8 + wn * 4 + a;  // global 32-row tile index
-      if constexpr (EPI == static_cast<int>(Epilogue::kSiluMul)) {
+    for (int jj = 0; jj < 4; ++jj) {
+      const int n = an * 32 + 8 * jj + 4 * kg;
+      const float2 p0 = src(2 * jj), p1 = src(2 * jj + 1);
+      float v[4] = {bf16_round(p0.x), bf16_round(p0.y), bf16_round(p1.x), bf16_round(p1.y)};
+      if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd)) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-          const int n = an * 16 + 8 * jj + 4 * kg;  // intermediate column
-          unsigned short o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = bf16_bits(silu_mul_bf16(acc[a][b][4 * jj + e], acc[a][b][4 * jj + 8 + e]));
-          *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
-              u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
-        }
-      } else {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int n = an * 32 + 8 * jj + 4 * kg;
-          unsigned short o[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float v = bf16_round(acc[a][b][4 * jj + e]);
-            if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd))
-              v = static_cast<float>(residual[(size_t)m * ldr + n + e]) + v;
-            o[e] = bf16_bits(v);
-          }
-          *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
-              u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
-        }
+        for (int e = 0; e < 4; ++e) v[e] = static_cast<float>(g.residual[(size_t)m * g.ldr + n + e]) + v[e];
       }
+      *reinterpret_cast<u32x2_t*>(g.y + (size_t)m * g.ldy + n) =
+          u32x2_t{bf16_bits(v[0]) | ((unsigned)bf16_bits(v[1]) << 16),
+                  bf16_bits(v[2]) | ((unsigned)bf16_bits(v[3]) << 16)};
     }
   }
 }
 
+// Epilogue of the whole block straight from the accumulators.
+template <int EPI>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[4][4], const Args& g, int nb, int mb) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      store_one_tile<EPI>([&](int p) { return make_float2(acc[a][b][2 * p], acc[a][b][2 * p + 1]); }, g, nb, mb, a,
+                          b);
+}
+
+__device__ __forceinline__ void zero(f32x16_t (&acc)[4][4]) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][b][j] = 0.f;
+}
+
+// ---- Split-K of the last round -------------------------------------------
+//
+// T output blocks on G CUs run ceil(T/G) rounds of whole-K blocks; when the
+// last round is partial (R = T mod G blocks, or all T when T < G, e.g. 80
+// blocks of the hidden-output projections at 2048 tokens) most CUs idle
+// through it.  The launch therefore runs the first T - R blocks one per
+// workgroup (the grouped, XCD-aware order of block_coords, so the ~32
+// workgroups of an XCD share weight and activation lines in its L2) and
+// splits each of the R last blocks into S = min(G / R, units / 4) chunks of
+// 128-K units, all blocks' chunk s covering the same K range so that they
+// share lines the same way.  The S workgroups of a split block each store
+// their fp32 accumulators to a workspace slot and count themselves in the
+// block's arrival word; once all S have arrived, workgroup s sums tiles
+// [16s/S, 16(s+1)/S) of the block over the S slots in chunk order and
+// stores them with the epilogue, then counts itself out; the last one out
+// clears both words.  R*S <= G, and whole-K blocks never wait, so every
+// split workgroup gets a CU; the waits are bounded anyway (a workgroup that
+// gives up records it in the error word and stores what it has).  The order
+// of every sum is fixed by (T, G), so results are bitwise reproducible.
+// Partials cross XCDs, whose L2s are not coherent with each other, so they
+// are written and read with device-coherent (sc1) accesses, the ones
+// agent-scope relaxed atomics use; no cache maintenance is needed.
+
+typedef unsigned int u32x2v_t __attribute__((ext_vector_type(2)));
+constexpr int kCoherent = 16;
+constexpr unsigned kRawBufferDword3 = 0x00020000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(unsigned char* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, (int)kRawBufferDword3);
+}
+
+// Block t of the grouped order (kGroupM token blocks, all weight blocks of a
+// group before the next group, token block fastest).
+__device__ __forceinline__ void tile_coords(int t, int n_blocks, int m_blocks, int& nb, int& mb) {
+  const int group = t / (kGroupM * n_blocks);
+  const int first_m = group * kGroupM;
+  const int group_m = min(m_blocks - first_m, kGroupM);
+  const int in_group = t - group * kGroupM * n_blocks;
+  mb = first_m + in_group % group_m;
+  nb = in_group / group_m;
+}
+
+struct Split {
+  unsigned* error;          // workspace word 0
+  unsigned* flags;          // arrival, departure word per split block
+  unsigned char* partials;  // kSkPartialBytes per split workgroup
+  unsigned partial_bytes;   // R * S * kSkPartialBytes
+  int dp;                   // blocks run whole (T - R)
+  int R;                    // blocks split
+  int S;                    // chunks per split block (1 = no split)
+  int units;                // 128-K units per block (KT / 4)
+};
+
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXStageBytes];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  f32x16_t acc[4][4];
+  zero(acc);
+
+  if (b < k.dp) {
+    // Whole block; workgroup b runs on XCD b % 8, so give each XCD a
+    // contiguous run of the grouped order.
+    const int t = k.dp % 8 == 0 ? (b % 8) * (k.dp / 8) + b / 8 : b;
+    int nb, mb;
+    tile_coords(t, g.n_blocks, g.m_blocks, nb, mb);
+    mainloop(acc, g, lds, nb, mb, 0, g.KT / 2);
+    store_tile<EPI>(acc, g, nb, mb);
+    return;
+  }
+  // Chunk-major order: all split blocks' chunk 0, then chunk 1, ...
+  const int r = b - k.dp;
+  const int chunk = r / k.R;
+  const int i = r % k.R;
+  int nb, mb;
+  tile_coords(k.dp + i, g.n_blocks, g.m_blocks, nb, mb);
+  const int u0 = chunk * k.units / k.S, u1 = (chunk + 1) * k.units / k.S;
+  mainloop(acc, g, lds, nb, mb, 2 * u0, 2 * u1);
+
+  // Publish this chunk's partial (slot chunk*R + i): quad q of tile (a, b)
+  // of thread tid at ((4*(4a+b) + q) * 256 + tid) * 16 bytes, so each store
+  // instruction writes 1 KB contiguously straight from four accumulators.
+  const __amdgpu_buffer_rsrc_t parts = partial_rsrc(k.partials, k.partial_bytes);
+  {
+    const unsigned slot = (unsigned)r * (unsigned)kSkPartialBytes;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int bb = 0; bb < 4; ++bb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          f32x4_t v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[a][bb][4 * q + e]));
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), parts, tid * 16,
+                                                 slot + ((a * 4 + bb) * 4 + q) * kThreads * 16, kCoherent);
+        }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  unsigned* arrive = k.flags + 2 * i;
+  unsigned* depart = arrive + 1;
+  if (tid == 0) {
+    __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned spins = 0;
+    while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)k.S) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > kSkSpinLimit) {
+        __hip_atomic_store(k.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+
+  // Sum this workgroup's share of the block's tiles over the S chunks.
+  const unsigned first = (unsigned)i * (unsigned)kSkPartialBytes;
+  const unsigned chunk_stride = (unsigned)k.R * (unsigned)kSkPartialBytes;
+  const int ab1 = (chunk + 1) * 16 / k.S;
+  for (int ab = chunk * 16 / k.S; ab < ab1; ++ab) {
+    f32x4_t sum[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < k.S; ++c) {
+      f32x4_t v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                               parts, tid * 16, first + c * chunk_stride + (ab * 4 + q) * kThreads * 16,
+                                               kCoherent));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum[q] += v[q];
+    }
+    store_one_tile<EPI>([&](int p) { return make_float2(sum[p >> 1][2 * (p & 1)], sum[p >> 1][2 * (p & 1) + 1]); },
+                        g, nb, mb, ab >> 2, ab & 3);
+  }
+  if (tid == 0 &&
+      __hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)k.S - 1) {
+    __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+inline Args make_args(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
+                      const void* residual, int ldr) {
+  Args g;
+  g.w = static_cast<const bf16x8_t*>(w);
+  g.x = static_cast<const __bf16*>(x);
+  g.y = static_cast<__bf16*>(y);
+  g.residual = static_cast<const __bf16*>(residual);
+  g.ldx = ldx;
+  g.ldy = ldy;
+  g.ldr = ldr;
+  g.M = M;
+  g.KT = K / kTileK;
+  g.n_blocks = N / BN;
+  g.m_blocks = (M + BM - 1) / BM;
+  return g;
+}
+
+// Blocks split and chunks per split block for T blocks of `units` 128-K
+// units on `grid` CUs (R = 0 or S = 1: no split).
+inline void split_plan(int T, int units, int grid, int* R, int* S) {
+  *R = grid > 0 ? T % grid : 0;
+  *S = 1;
+  if (*R == 0) return;
+  int s = grid / *R;
+  if (s > units / 4) s = units / 4;
+  if (s < 2) {
+    *R = 0;
+    return;
+  }
+  *S = s;
+}
+
+// `grid` = CUs available to the split (0: no split, no workspace needed).
 template <int EPI>
 hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
-                  const void* residual, int ldr, hipStream_t stream) {
-  const int n_blocks = N / BN;
-  const int m_blocks = (M + BM - 1) / BM;
-  gemm_wdx_kernel<EPI><<<dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream>>>(
-      static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
-      static_cast<const __bf16*>(residual), ldr, M, K / kTileK, n_blocks, m_blocks);
+                  const void* residual, int ldr, void* workspace, int grid, hipStream_t stream) {
+  const Args g = make_args(w, N, K, x, M, ldx, y, ldy, residual, ldr);
+  const int T = g.n_blocks * g.m_blocks;
+  Split k;
+  k.units = g.KT / 4;
+  split_plan(T, k.units, workspace != nullptr ? grid : 0, &k.R, &k.S);
+  k.dp = T - k.R;
+  auto* ws = static_cast<unsigned char*>(workspace);
+  k.error = reinterpret_cast<unsigned*>(ws);
+  k.flags = ws != nullptr ? reinterpret_cast<unsigned*>(ws + kSkFlagsOffset) : nullptr;
+  k.partials = ws != nullptr ? ws + kSkPartialsOffset : nullptr;
+  k.partial_bytes = (unsigned)((size_t)k.R * k.S * kSkPartialBytes);
+  gemm_wdx_kernel<EPI><<<dim3(k.dp + k.R * k.S), dim3(kThreads), 0, stream>>>(g, k);
   return hipGetLastError();
 }
 
@@ -722,17 +941,68 @@ hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx
 
 }  // namespace
 
+namespace {
+
+bool sk_shape(int M, int N, int K) { return M > kGemmBM && N % wdx::BN == 0 && K % (2 * wdx::BK) == 0; }
+
+// Persistent stream-K grid on `device`: every CU's resident workgroups
+// (the kernel holds 512 registers per lane, so one per CU), capped by the
+// workspace's flag capacity.  Cached per device.
+hipError_t sk_grid(int device, int* grid_out) {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  if (device >= (int)cache.size()) cache.resize(device + 1, 0);
+  if (cache[device] == 0) {
+    int cus = 0, per_cu = 0;
+    hipError_t err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return err;
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, reinterpret_cast<const void*>(&wdx::gemm_wdx_kernel<0>), wdx::kThreads, 0);
+    if (err != hipSuccess) return err;
+    int grid = cus * (per_cu > 0 ? per_cu : 1);
+    cache[device] = grid < kSkMaxGrid ? grid : kSkMaxGrid;
+  }
+  *grid_out = cache[device];
+  return hipSuccess;
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int device, int M, int N, int K, hipError_t* status) {
+  *status = hipSuccess;
+  if (!sk_shape(M, N, K)) return 0;
+  int grid = 0;
+  *status = sk_grid(device, &grid);
+  if (*status != hipSuccess) return 0;
+  return kSkPartialsOffset + (size_t)grid * kSkPartialBytes;
+}
+
 hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
-                              Epilogue epi, const void* residual, int ldr, hipStream_t stream) {
-  if (M > kGemmBM && N % wdx::BN == 0 && K % (2 * wdx::BK) == 0) {
+                              Epilogue epi, const void* residual, int ldr, void* workspace, size_t ws_bytes,
+                              hipStream_t stream) {
+  if (sk_shape(M, N, K)) {
+    // With a workspace, the partial last round is split over every CU (as
+    // many as the workspace has partial slots for).
+    int grid = 0;
+    if (workspace != nullptr && ws_bytes > kSkPartialsOffset) {
+      int device = 0;
+      hipError_t err = hipGetDevice(&device);
+      if (err != hipSuccess) return err;
+      err = sk_grid(device, &grid);
+      if (err != hipSuccess) return err;
+      const size_t fit = (ws_bytes - kSkPartialsOffset) / kSkPartialBytes;
+      if ((size_t)grid > fit) grid = (int)fit;
+    }
+    void* ws = grid > 0 ? workspace : nullptr;
     switch (epi) {
       case Epilogue::kSiluMul:
-        return wdx::launch<1>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+        return wdx::launch<1>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
       case Epilogue::kResidualAdd:
-        return wdx::launch<2>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+        return wdx::launch<2>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
       case Epilogue::kNone:
       default:
-        return wdx::launch<0>(w, N, K, x, M, ldx, y, ldy, residual, ldr, stream);
+        return wdx::launch<0>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
     }
   }
   if (M > kGemmBM && N % big::BN == 0 && K % big::BK == 0) {

@@ -39,12 +39,43 @@ def stream_handle() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+_prefill_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def prefill_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor | None:
+    """The stream-K workspace of the prefill GEMM for the current stream of
+    `device` (zero-filled once, left zero-filled by every call), or None when
+    the shape does not use one.  One per (device, stream), because calls that
+    share a workspace must be stream-ordered."""
+    nbytes = _lib.load().lsk_workspace_bytes(_lib.OP_LINEAR, m, n, k)
+    if nbytes == 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle() or 0)
+    ws = _prefill_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+        _prefill_workspaces[key] = ws
+    return ws
+
+
+def linear_error(workspace: torch.Tensor) -> int:
+    """Read and clear the error word of a prefill workspace (0 = no bounded
+    wait gave up since the last read).  Synchronous."""
+    err = ctypes.c_int(0)
+    _lib.check(_lib.load().lsk_linear_error(workspace.data_ptr(), ctypes.byref(err)), "lsk_linear_error")
+    return err.value
+
+
 def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NONE,
-           residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+           residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+           workspace: torch.Tensor | None | str = "auto") -> torch.Tensor:
     """out[..., N'] = epilogue(x[..., K] . W^T) on the GPU.
 
     epilogue EPI_NONE (N' = N), EPI_SILU_MUL (gate_up layout, N' = N/2,
-    SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection)."""
+    SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection).
+    workspace: "auto" uses the per-stream stream-K workspace for prefill
+    shapes (prefill_workspace), None runs one workgroup per output block, a
+    uint8 device tensor is used as given."""
     if not isinstance(weight, PackedWeight):
         raise ValueError("weight must be a PackedWeight (pack it with leanstack_amd.layout / leanserve)")
     lib = _lib.load()
@@ -64,12 +95,20 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
         if rm != m:
             raise ValueError(f"residual has {rm} rows, x has {m}")
         res_ptr = r2.data_ptr()
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError(f"workspace must be 'auto', None or a tensor, not {workspace!r}")
+        workspace = prefill_workspace(x.device, m, weight.n, weight.k) if m > _lib.DECODE_MAX_M else None
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        _require_device(workspace, "workspace")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     status = lib.lsk_linear_bf16(
         weight.data.data_ptr(), weight.layout, weight.n, weight.k,
         x2.data_ptr(), m, ldx,
         out.data_ptr(), n_out,
         epilogue, res_ptr, ldr,
-        None, 0, stream_handle(),
+        ws_ptr, ws_bytes, stream_handle(),
     )
     _lib.check(status, "lsk_linear_bf16")
     return out

@@ -27,11 +27,11 @@ PROJ = {
 }
 
 
-def _gpu_linear(x, w, layout=_lib.LAYOUT_MFMA16X32, epilogue=_lib.EPI_NONE, residual=None):
+def _gpu_linear(x, w, layout=_lib.LAYOUT_MFMA16X32, epilogue=_lib.EPI_NONE, residual=None, workspace="auto"):
     dev = torch.device("cuda:0")
     pw = PackedWeight.from_rowmajor(w.to(dev), layout)
     res = residual.to(dev) if residual is not None else None
-    y = kernels.linear(x.to(dev), pw, epilogue=epilogue, residual=res)
+    y = kernels.linear(x.to(dev), pw, epilogue=epilogue, residual=res, workspace=workspace)
     torch.cuda.synchronize()
     return y.cpu()
 
@@ -210,3 +210,46 @@ def test_prefill_m2048_full_shapes(gpu, name):
         y = _gpu_linear(x, w)
         expect = ref.linear(x, w)
     assert_parity(y, expect, f"{name} prefill M=2048")
+
+
+@pytest.mark.parametrize("name", sorted(PROJ) + ["gate_up_proj"])
+@pytest.mark.parametrize("m", [300, 2048])
+def test_prefill_one_block_per_workgroup(gpu, name, m):
+    """The data-parallel prefill kernel (no workspace) at every projection shape."""
+    if name == "gate_up_proj":
+        n, k = 2 * G.intermediate_size, G.hidden_size
+        w = weight(n, k, seed=83)
+        x = activations(m, k, seed=830)
+        y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL, workspace=None)
+        expect = ref.silu_mul(ref.linear(x, w), G.intermediate_size)
+    else:
+        n, k = PROJ[name]
+        w = weight(n, k, seed=84)
+        x = activations(m, k, seed=840)
+        y = _gpu_linear(x, w, workspace=None)
+        expect = ref.linear(x, w)
+    assert_parity(y, expect, f"{name} data-parallel M={m}")
+
+
+def test_split_k_workspace_contract(gpu):
+    """Split-K: residual epilogue through split blocks, flags left zero,
+    error word clear, and two calls on one workspace give identical bits."""
+    dev = torch.device("cuda:0")
+    m, n, k = 2048, G.hidden_size, G.intermediate_size  # 80 blocks, each split in 3 K chunks
+    w = weight(n, k, seed=85)
+    x = activations(m, k, seed=850)
+    r = activations(m, n, seed=851)
+    pw = PackedWeight.from_rowmajor(w.to(dev))
+    nbytes = _lib.load().lsk_workspace_bytes(_lib.OP_LINEAR, m, n, k)
+    assert nbytes > 0
+    ws = torch.zeros(nbytes, device=dev, dtype=torch.uint8)
+    y1 = kernels.linear(x.to(dev), pw, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r.to(dev), workspace=ws)
+    y2 = kernels.linear(x.to(dev), pw, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r.to(dev), workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert_parity(y1.cpu(), r + ref.linear(x, w), "down+residual split-K M=2048")
+    flags = ws[256:8192].view(torch.int32)
+    assert int(flags.abs().sum().item()) == 0
+    assert kernels.linear_error(ws) == 0
+    with pytest.raises(ValueError):
+        kernels.linear(x.to(dev), pw, workspace=ws[: nbytes // 2])
