@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 1
+#define LSK_ABI_VERSION 2
 
 enum lsk_layout {
   LSK_LAYOUT_ROWMAJOR = 0,        /* plain W[N][K]; accepted by the packer only */
@@ -164,7 +164,7 @@ typedef struct lsk_projection {
   const void* w_packed;  /* packed weights, as for lsk_linear_bf16 */
   int layout_id;
   int N;
-  int K;                 /* K/32 must be a multiple of 8 and >= 8 */
+  int K;                 /* a multiple of 512 */
   const void* x;         /* input rows [M][K] at stride ldx */
   int ldx;
   void* y;               /* output rows at stride ldy */
@@ -180,9 +180,11 @@ typedef struct lsk_projection {
 /* Device bytes of a program of `count` projections. */
 size_t lsk_stack_program_bytes(int count);
 
-/* Device workspace bytes of a program of `count` projections.  The caller
- * zeroes it once before the first launch; every launch leaves it zeroed
- * (except the error word, see lsk_stack_error). */
+/* Device workspace bytes of a program of `count` projections on the current
+ * device (it holds per-CU progress words and cross-CU partial sums, so it is
+ * sized by the CU count).  The caller zeroes it once before the first
+ * launch; every launch leaves its synchronisation words zeroed again (the
+ * error word aside, see lsk_stack_error). */
 size_t lsk_stack_workspace_bytes(int count);
 
 /* Validate `projections` (host array) and upload the program to program_dev

@@ -249,11 +249,13 @@ int stack_grid(int device, size_t lds_bytes, int* grid_out) {
     hipError_t err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
     if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute(multiprocessor count)");
     int per_cu = 0;
-    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, lsk::stack_kernel_symbol(), lsk::kStackWaves * 64,
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, lsk::stack_kernel_symbol(), lsk::stack_threads(),
                                                        lds_bytes);
     if (err != hipSuccess) return hip_fail(err, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (cus <= 0 || per_cu <= 0) return fail(LSK_ERR_HIP, "stack kernel cannot be resident (cus=%d, per_cu=%d)", cus, per_cu);
-    cache[device] = cus * per_cu;
+    // Every workgroup must be resident at once (they wait for each other).
+    const int grid = cus * per_cu;
+    cache[device] = grid < lsk::kStackMaxGrid ? grid : lsk::kStackMaxGrid;
   }
   *grid_out = cache[device];
   return LSK_OK;
@@ -271,13 +273,17 @@ size_t lsk_stack_program_bytes(int count) { return count > 0 ? stack_program_byt
 
 size_t lsk_stack_workspace_bytes(int count) {
   if (count <= 0) return 0;
-  const size_t words = (size_t)lsk::kStackWsCounters + (size_t)count;
-  return (words * sizeof(unsigned) + 255) / 256 * 256;
+  int device = 0, grid = 0;
+  if (hipGetDevice(&device) != hipSuccess) return 0;
+  if (stack_grid(device, lsk::stack_lds_bytes(), &grid) != LSK_OK) return 0;
+  return lsk::kStackWsBytes(count, grid);
 }
 
 int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void* program_dev, size_t program_bytes) {
   g_last_error.clear();
   if (projections == nullptr || count <= 0) return fail(LSK_ERR_INVALID, "empty stack program");
+  if (count > lsk::kStackMaxProjections)
+    return fail(LSK_ERR_INVALID, "stack program of %d projections (at most %d)", count, lsk::kStackMaxProjections);
   if (M < 1 || M > lsk::kDecodeMaxM) return fail(LSK_ERR_INVALID, "stack M=%d must be in 1..%d", M, lsk::kDecodeMaxM);
   if (program_dev == nullptr || program_bytes < stack_program_bytes(count) || !aligned(program_dev, 64))
     return fail(LSK_ERR_INVALID, "program buffer needs %zu bytes, 64-byte aligned", stack_program_bytes(count));
@@ -286,13 +292,13 @@ int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void*
   prog->count = count;
   prog->M = M;
   prog->magic = lsk::kStackMagic;
-  int item_begin = 0;
   for (int i = 0; i < count; ++i) {
     const lsk_projection& p = projections[i];
     if (int st = check_shape(p.layout_id, p.N, p.K)) return fail(st, "projection %d: %s", i, g_last_error.c_str());
     const int KT = p.K / lsk::kTileK;
-    if (KT % lsk::kStackWaves != 0)
-      return fail(LSK_ERR_INVALID, "projection %d: K/32=%d must be a multiple of %d", i, KT, lsk::kStackWaves);
+    if (KT % lsk::kStackSegTiles != 0)
+      return fail(LSK_ERR_INVALID, "projection %d: K=%d must be a multiple of %d", i, p.K,
+                  lsk::kStackSegTiles * lsk::kTileK);
     if (p.epilogue != LSK_EPI_NONE && p.epilogue != LSK_EPI_SILU_MUL && p.epilogue != LSK_EPI_RESIDUAL_ADD)
       return fail(LSK_ERR_INVALID, "projection %d: unknown epilogue %d", i, p.epilogue);
     if ((p.epilogue == LSK_EPI_SILU_MUL) != (p.layout_id == LSK_LAYOUT_MFMA16X32_GATEUP))
@@ -324,12 +330,9 @@ int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void*
     d.ldr = p.ldr;
     d.epi = p.epilogue;
     d.rbw = p.epilogue == LSK_EPI_SILU_MUL ? 2 : 1;
-    d.items = p.N / lsk::kTileRows / d.rbw;
-    d.item_begin = item_begin;
+    d.units = p.N / lsk::kTileRows / d.rbw;
     d.dep = p.depends_on;
-    item_begin += d.items;
   }
-  prog->total_items = item_begin;
   hipError_t err = hipMemcpy(program_dev, host.data(), host.size(), hipMemcpyHostToDevice);
   if (err != hipSuccess) return hip_fail(err, "hipMemcpy(stack program)");
   return LSK_OK;
@@ -338,14 +341,19 @@ int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void*
 int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws_bytes, void* hip_stream) {
   g_last_error.clear();
   if (program_dev == nullptr || count <= 0) return fail(LSK_ERR_INVALID, "null or empty stack program");
-  if (workspace == nullptr || ws_bytes < lsk_stack_workspace_bytes(count) || !aligned(workspace, 256))
-    return fail(LSK_ERR_WORKSPACE, "stack workspace needs %zu bytes, 256-byte aligned", lsk_stack_workspace_bytes(count));
+  // A workspace below the one-workgroup size is wrong on any device.
+  if (workspace == nullptr || ws_bytes < lsk::kStackWsBytes(count, 1) || !aligned(workspace, 256))
+    return fail(LSK_ERR_WORKSPACE, "stack workspace needs lsk_stack_workspace_bytes(%d) bytes, 256-byte aligned",
+                count);
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
   const size_t lds = lsk::stack_lds_bytes();
   int grid = 0;
   if (int st = stack_grid(device, lds, &grid)) return st;
+  if (ws_bytes < lsk::kStackWsBytes(count, grid))
+    return fail(LSK_ERR_WORKSPACE, "stack workspace needs %zu bytes on this device (got %zu)",
+                lsk::kStackWsBytes(count, grid), ws_bytes);
   err = lsk::launch_decode_stack(static_cast<const lsk::StackProgram*>(program_dev), static_cast<unsigned*>(workspace),
                                  grid, lds, static_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess) return hip_fail(err, "stack kernel launch");

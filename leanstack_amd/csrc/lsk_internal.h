@@ -34,11 +34,27 @@ constexpr int kSkMaxGrid = (int)((kSkPartialsOffset - kSkFlagsOffset) / 4);
 constexpr unsigned kSkSpinLimit = 1u << 22;
 
 // Persistent decode-step kernel (stack.hip).
-constexpr int kStackWaves = 8;        // waves per workgroup (they split K)
-constexpr int kStackWsError = 0;      // workspace word: nonzero after a bounded wait gave up
-constexpr int kStackWsExit = 1;       // workspace word: workgroups finished (reset by the last)
-constexpr int kStackWsCounters = 16;  // workspace words from here: done[p], items published
-constexpr unsigned kStackMagic = 0x4c534b31u;
+constexpr int kStackComputeWaves = 8;  // compute waves per workgroup (+1 control wave)
+constexpr int kStackSegTiles = 16;     // k-tiles per K segment of a work pair (K % 512 == 0)
+constexpr int kStackMaxProjections = 512;
+constexpr unsigned kStackMagic = 0x4c534b32u;
+// Workspace (32-bit words unless noted): error word, exit counter, one
+// progress word per workgroup, then one partial flag per (projection,
+// workgroup), then one partial slot (kStackPartialBytes) per (projection,
+// workgroup).
+constexpr int kStackWsError = 0;      // nonzero after a bounded wait gave up
+constexpr int kStackWsExit = 1;       // workgroups finished (reset by the last)
+constexpr int kStackWsDetail = 8;     // 8 words: first failed wait (workgroup + 1, code, state)
+constexpr int kStackWsProgress = 64;  // G words: projections completed by each workgroup
+constexpr int kStackMaxGrid = 2048 - kStackWsProgress;
+constexpr size_t kStackPartialBytes = 2048;  // 2 row-blocks x 64 lanes x 16 bytes
+constexpr int kStackWsFlags = 2048;  // count x G words from here
+__host__ __device__ constexpr size_t kStackWsPartialsOffset(int count, int G) {
+  return (((size_t)kStackWsFlags + (size_t)count * G) * 4 + 255) / 256 * 256;
+}
+__host__ __device__ constexpr size_t kStackWsBytes(int count, int G) {
+  return kStackWsPartialsOffset(count, G) + (size_t)count * G * kStackPartialBytes;
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
@@ -49,20 +65,17 @@ struct StackDesc {
   __bf16* y;
   const __bf16* res;
   int KT, ldx, ldy, ldr;
-  int epi;         // Epilogue
-  int rbw;         // row-blocks per item: 1, or 2 for a SiLU gate/up pair
-  int items;       // work items (row-block groups) of this projection
-  int item_begin;  // global index of its first item
-  int dep;         // -1, or: every projection <= dep must finish first
-  int pad[3];
+  int epi;    // Epilogue
+  int rbw;    // row-blocks per unit: 1, or 2 for a SiLU gate/up pair
+  int units;  // N / (16 * rbw)
+  int dep;    // -1, or: every projection <= dep completes before this one reads x / residual
 };
 
 struct StackProgram {
   int count;
   int M;
-  int total_items;
   unsigned magic;
-  int pad[12];
+  int pad[13];
   StackDesc desc[1];  // `count` entries follow the header
 };
 
@@ -70,6 +83,7 @@ hipError_t launch_decode_stack(const StackProgram* prog, unsigned* ws, int grid,
                                hipStream_t stream);
 size_t stack_lds_bytes();
 const void* stack_kernel_symbol();
+int stack_threads();
 
 // Argmax partial written by each lm_head workgroup: (score, index).
 struct ArgmaxPartial {

@@ -1,37 +1,54 @@
 // Persistent decode-step kernel: a whole sequence of projections (e.g. the
 // 36 layers x {QKV, o_proj, gate_up + SiLU*up, down} of a decode or verify
-// step at M <= 16) in ONE launch.
+// step at M <= 16) in ONE launch, streaming weights from HBM without a gap at
+// projection boundaries.
 //
 // Why: each projection is only 21-100 MB, 3-14 us of HBM time, so separate
-// launches pay the ramp-up/tail of every kernel (about 2 us of fixed cost per
-// launch even for an ideal streaming kernel).  Here one workgroup per CU
-// walks a global list of work items in projection order, and every wave
-// keeps the next chunk of weight tiles in flight while it computes the
-// current one -- including across projection boundaries, where the weights
-// of the next projection stream in while the wave waits for the previous
-// projection's output (its activations).  Weights never depend on
-// activations, so the dependency wait overlaps HBM traffic.
+// launches pay every kernel's ramp-up and tail (2-3 us per launch).  Here one
+// workgroup per CU walks its share of every projection in order, and the
+// weight stream of the next projection is already in flight while the
+// current one finishes: weights never depend on activations.
 //
-// Work item: one row-block group of one projection (16 output rows, or a
-// 16-row gate/up pair for SiLU*up) over the full K.  The 8 waves of the
-// workgroup split K, accumulate with v_mfma_f32_16x16x32_bf16 exactly as the
-// single-projection decode kernel does (decode.hip), reduce through LDS in
-// wave order (bitwise reproducible) and wave 0 applies the epilogue.
+// Work split.  A projection of U units (16 weight rows, or a 32-row gate/up
+// pair for SiLU*up) and K = NS segments of 512 is a list of U*NS
+// (unit, segment) pairs, unit-major; workgroup g takes pairs
+// [g*P/G, (g+1)*P/G).  Every CU so streams the same number of bytes of every
+// projection (within one pair), whatever U is -- 160 units of o_proj and
+// down_proj against 256 CUs included.
 //
-// Dependencies: projection p may name an earlier projection d whose output
-// it reads.  Before the first chunk of an item of p, wave 0 of the workgroup
-// polls done[q] for every q <= d until all their items are finished; the
-// other waves wait at a barrier with their weight loads still in flight.
-// After the epilogue, wave 0 waits for its output stores to complete and
-// increments done[p].  Activations, residuals and outputs are read and
-// written with coherent (agent-scope) accesses, so no cache maintenance is
-// needed between producer and consumer workgroups.  The grid is sized to what the device holds at once
-// (CUs x resident workgroups per CU, from the occupancy query), each
-// workgroup processes its items in increasing projection order, so the
-// dependency graph always drains; every wait is still bounded and records
-// an error instead of spinning forever.  The last workgroup to
-// finish resets the counters, so the workspace is reusable by the next
-// launch (and by graph replays) without a memset.
+// Roles inside the workgroup (9 waves):
+//  * 8 compute waves.  Wave w takes k-tiles 2w, 2w+1 of every segment, for
+//    every row-block of the pair, so each wave's stream of 1 KB weight tiles
+//    is fixed by the program.  A wave keeps kRing tile loads in flight in
+//    registers and refills a slot as soon as it is multiplied, so the only
+//    memory waits it has are for its own oldest weight load.  Activation
+//    fragments come from LDS (staged by the control wave); accumulators of a
+//    finished unit range go to LDS for the control wave.
+//  * 1 control wave.  It stages each pair's activation segment into a ring
+//    of LDS slots (coherent loads, after the projection's dependency is
+//    met), sums the 8 compute waves' partials of each unit range in wave
+//    order, and finishes units: a unit wholly inside the workgroup's range
+//    is stored with its epilogue; a unit that later workgroups finish is
+//    "owned" here (this workgroup has its segment 0): the owner waits for
+//    their fp32 partials, adds them in workgroup order and stores; a unit
+//    this workgroup enters mid-K is published as a partial for its owner.
+//    After its last unit range of a projection it publishes its progress
+//    word (projections completed).  A projection that depends on q starts
+//    staging activations once every workgroup's progress exceeds q.  The
+//    control wave never blocks on one of these while other work is ready,
+//    so a workgroup always finishes what other workgroups wait for.
+//
+// Every sum has a fixed order (waves, then workgroups), so results are
+// bitwise reproducible.  Activations, residuals, outputs, partials and
+// progress cross XCDs, whose L2s are not coherent with each other, so they
+// are read and written with agent-scope relaxed atomics (device-coherent
+// loads and stores; no cache maintenance).  Owners wait only for later
+// workgroups' partials and dependencies point to earlier projections, so
+// the waits always drain with the whole grid resident (one workgroup per
+// CU); every wait is bounded anyway and records an error instead of
+// spinning forever.  The last workgroup out clears the progress words, and
+// owners clear the partial flags they consumed, so the workspace is
+// reusable by the next launch (and by graph replays) without a memset.
 
 #include <hip/hip_runtime.h>
 
@@ -42,27 +59,34 @@ namespace {
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = kStackWaves;
-constexpr int kChunkTiles = 12;         // weight tiles per wave per chunk (register budget)
-constexpr unsigned kSpinLimit = 1u << 20;  // about a second of polling
+constexpr int kCompute = kStackComputeWaves;          // 8
+constexpr int kThreads = (kCompute + 2) * 64;         // + stager and finisher waves
+constexpr int kSeg = kStackSegTiles;                  // 16 k-tiles (512 K) per segment
+constexpr int kWaveTiles = kSeg / kCompute;           // 2 k-tiles per compute wave per segment
+constexpr int kRing = 16;                             // weight tiles in flight per compute wave
+constexpr int kXRow = kSeg * kTileK * 2 + 16;         // LDS bytes per activation row (+16: bank skew)
+constexpr int kXBytes = 116 * 1024;                   // staged activation segments (M rows each)
+constexpr int kMaxXSlots = 16;
+constexpr int kRedSlots = 2;
+constexpr unsigned kSpinLimit = 1u << 22;   // polls of one LDS or partial-flag wait
+constexpr unsigned kIdleLimit = 1u << 20;   // control-wave rounds without progress
 
-// Pointers come from the program in memory, so the compiler cannot infer
-// their address space; spell it out so weight loads are global_* ops.  (A
-// flat load also counts in lgkmcnt, and every barrier's lgkmcnt(0) wait
-// would then drain the whole weight prefetch.)
-typedef __attribute__((address_space(1))) bf16x8_t global_bf16x8;
 
-__device__ __forceinline__ bf16x8_t load_weight_tile(const bf16x8_t* p) {
-  return __builtin_nontemporal_load((const global_bf16x8*)(p));
+template <int I>
+struct IntC {
+  static constexpr int value = I;
+};
+// f(IntC<0>{}), ..., f(IntC<N-1>{}) in order.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void unroll(F&& f) {
+  if constexpr (I < N) {
+    f(IntC<I>{});
+    unroll<N, I + 1>(f);
+  }
 }
-
-__device__ __forceinline__ bf16x8_t masked(bf16x8_t v, unsigned keep) {
-  u32x4_t u = __builtin_bit_cast(u32x4_t, v);
-  u &= keep;
-  return __builtin_bit_cast(bf16x8_t, u);
-}
+typedef __attribute__((address_space(1))) unsigned long long global_u64;
+typedef __attribute__((address_space(1))) unsigned global_u32;
 
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -81,88 +105,6 @@ __device__ __forceinline__ float silu_mul_bf16(float g_acc, float u_acc) {
   return bf16_round(s * u);
 }
 
-// Wave-uniform position in the chunk sequence.
-struct Cursor {
-  int gi;     // global item index (>= total: finished)
-  int p;      // projection of the item
-  int item;   // item index inside projection p
-  int kb;     // first k-tile of this wave's range of the item
-  int len;    // k-tiles in this wave's range
-  int nc;     // chunks the range is cut into (balanced sizes)
-  int ci;     // current chunk
-  int kt0;    // first k-tile of the chunk
-  int nkt;    // k-tiles in the chunk
-  int first;  // 1 on the first chunk of this wave's part of the item
-};
-
-struct Ctx {
-  const StackDesc* desc;
-  int count;
-  int total;
-  int wave;
-  int lane;
-};
-
-__device__ __forceinline__ void set_chunk(Cursor& c) {
-  c.kt0 = c.kb + (c.len * c.ci) / c.nc;
-  c.nkt = c.kb + (c.len * (c.ci + 1)) / c.nc - c.kt0;
-}
-
-// Start the wave's part of global item gi (searching forward from projection p).
-// Every wave's range has the same length (K/32 is a multiple of the wave
-// count), so all waves see the same chunk count and meet at the same barriers.
-__device__ __forceinline__ void open_item(Cursor& c, const Ctx& x, int gi, int p) {
-  c.gi = gi;
-  if (gi >= x.total) return;
-  while (p + 1 < x.count && gi >= x.desc[p + 1].item_begin) ++p;
-  c.p = p;
-  c.item = gi - x.desc[p].item_begin;
-  c.len = x.desc[p].KT / kWaves;
-  c.kb = c.len * x.wave;
-  const int cap = kChunkTiles / x.desc[p].rbw;
-  c.nc = (c.len + cap - 1) / cap;
-  c.ci = 0;
-  c.first = 1;
-  set_chunk(c);
-}
-
-__device__ __forceinline__ void advance(Cursor& c, const Ctx& x) {
-  if (c.ci + 1 < c.nc) {
-    ++c.ci;
-    c.first = 0;
-    set_chunk(c);
-  } else {
-    open_item(c, x, c.gi + gridDim.x, c.p);
-  }
-}
-
-__device__ __forceinline__ bool is_last(const Cursor& c) { return c.ci + 1 == c.nc; }
-
-__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
-  return (unsigned)bf16_bits(lo) | ((unsigned)bf16_bits(hi) << 16);
-}
-
-template <int RBW>
-__device__ __forceinline__ void issue_weights(bf16x8_t (&buf)[kChunkTiles], const StackDesc& d, const Cursor& c,
-                                              int lane) {
-  const bf16x8_t* base = d.w + ((size_t)c.item * RBW * d.KT + c.kt0) * 64 + lane;
-#pragma unroll
-  for (int t = 0; t < kChunkTiles / RBW; ++t) {
-    if (t < c.nkt) {
-#pragma unroll
-      for (int r = 0; r < RBW; ++r) buf[t * RBW + r] = load_weight_tile(base + ((size_t)r * d.KT + t) * 64);
-    }
-  }
-}
-
-// Activations and outputs cross workgroups (and XCDs, whose L2s are not
-// coherent with each other), so every access to them is an agent-scope
-// relaxed atomic: coherent loads and stores that need no L2 write-back or
-// invalidate.  (Fence-based release/acquire would write back and invalidate
-// a whole L2 per item, which costs far more than the item itself.)
-// Global-address-space view, so these become global_* (not flat_*) ops.
-typedef __attribute__((address_space(1))) unsigned long long global_u64;
-
 __device__ __forceinline__ unsigned long long coherent_load64(const void* p) {
   return __hip_atomic_load((const global_u64*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -171,189 +113,606 @@ __device__ __forceinline__ void coherent_store64(void* p, unsigned long long v) 
   __hip_atomic_store((global_u64*)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ bf16x8_t coherent_frag(const bf16x8_t* p, unsigned long long keep) {
-  const unsigned long long lo = coherent_load64(p) & keep;
-  const unsigned long long hi = coherent_load64(reinterpret_cast<const unsigned long long*>(p) + 1) & keep;
-  u32x4_t u{(unsigned)lo, (unsigned)(lo >> 32), (unsigned)hi, (unsigned)(hi >> 32)};
-  return __builtin_bit_cast(bf16x8_t, u);
+__device__ __forceinline__ unsigned coherent_load32(const unsigned* p) {
+  return __hip_atomic_load((const global_u32*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void issue_x(bf16x8_t (&xv)[kChunkTiles], const StackDesc& d, const Cursor& c, int M,
-                                        int lane) {
-  const int m = lane & 15;
-  const int g = lane >> 4;
-  const unsigned long long keep = m < M ? ~0ull : 0ull;
-  const bf16x8_t* row = reinterpret_cast<const bf16x8_t*>(d.x + (size_t)(m < M ? m : 0) * d.ldx) + g;
-  const int cap = kChunkTiles / d.rbw;
-#pragma unroll
-  for (int t = 0; t < kChunkTiles; ++t) {
-    if (t < c.nkt && t < cap) xv[t] = coherent_frag(row + (c.kt0 + t) * 4, keep);
-  }
+__device__ __forceinline__ void coherent_store32(unsigned* p, unsigned v) {
+  __hip_atomic_store((global_u32*)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int RBW>
-__device__ __forceinline__ void consume(f32x4_t (&acc)[2], const bf16x8_t (&buf)[kChunkTiles],
-                                        const bf16x8_t (&xv)[kChunkTiles], int nkt) {
-#pragma unroll
-  for (int t = 0; t < kChunkTiles / RBW; ++t) {
-    if (t < nkt) {
-#pragma unroll
-      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(buf[t * RBW + r], xv[t], acc[r]);
-    }
-  }
+// Optional event timestamps (build with -DLSK_STACK_TRACE): word
+// (g * count + p) * 8 + event of a buffer placed right after the workspace
+// receives the constant-clock time of the event for workgroup g, projection p.
+#ifdef LSK_STACK_TRACE
+#define LSK_TRACE(ws_, count_, G_, g_, p_, ev_, lane_)                                                             \
+  do {                                                                                                            \
+    if ((lane_) == 0)                                                                                             \
+      __hip_atomic_store((global_u32*)((ws_) + kStackWsBytes((count_), (G_)) / 4 +                                \
+                                       ((size_t)(g_) * (count_) + (p_)) * 8 + (ev_)),                             \
+                         (unsigned)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); \
+  } while (0)
+#else
+#define LSK_TRACE(ws_, count_, G_, g_, p_, ev_, lane_) \
+  do {                                                 \
+  } while (0)
+#endif
+
+// Wave-uniform copy of a value the compiler cannot prove uniform (an LDS
+// load) but that is, so branches on it stay scalar.
+__device__ __forceinline__ unsigned uni(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
+
+// LDS words shared by the waves (relaxed workgroup-scope atomics: ds ops of
+// one wave execute in order, so flag/data ordering only needs the writer's
+// lgkmcnt wait before the flag).
+__device__ __forceinline__ unsigned lds_load(const unsigned* p) {
+  return uni(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+}
+__device__ __forceinline__ void lds_store(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_add(unsigned* p, unsigned v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Wave 0, after the LDS reduction: write the item's outputs and publish it.
-__device__ __forceinline__ void finish_item(const StackDesc& d, int item, const f32x4_t (&acc)[2], int M, int lane,
-                                            unsigned* done_p) {
-  const int m = lane & 15;
-  const int g = lane >> 4;
-  if (m < M) {
-    const int n = item * 16 + 4 * g;  // output column (intermediate index for SiLU*up)
-    f32x4_t v;
-    if (d.epi == static_cast<int>(Epilogue::kSiluMul)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = silu_mul_bf16(acc[0][i], acc[1][i]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = bf16_round(acc[0][i]);
-      if (d.epi == static_cast<int>(Epilogue::kResidualAdd)) {
-        const unsigned long long r = coherent_load64(d.res + (size_t)m * d.ldr + n);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          v[i] += __builtin_bit_cast(float, (unsigned)((r >> (16 * i)) & 0xffffu) << 16);
+// Activation slot i holds the M rows of one pair's segment at
+// xbuf + i * M * kXRow; there are min(kMaxXSlots, kXBytes / (M * kXRow)).
+__host__ __device__ constexpr int x_slots(int M) {
+  return kXBytes / (M * kXRow) < kMaxXSlots ? kXBytes / (M * kXRow) : kMaxXSlots;
+}
+
+// What the compute waves need of a projection, copied to LDS at launch so
+// their cursors never issue a vector load (which would disturb the weight
+// ring's wait count).
+struct SeqDesc {
+  const bf16x8_t* w;
+  int units;
+  short KT, rbw;
+};
+
+struct Shared {
+  SeqDesc seq[kStackMaxProjections];
+  unsigned char xbuf[kXBytes];                         // staged activation segments
+  f32x4_t red[kRedSlots][kCompute][2][64];             // compute-wave partials of a unit range
+  unsigned x_ready[kMaxXSlots];                        // pair sequence number + 1 of the slot's content
+  unsigned x_done[kMaxXSlots];                         // compute waves done reading the slot
+  unsigned red_count[kRedSlots];                       // compute waves that wrote the slot
+  unsigned red_next[kRedSlots];                        // unit-range number the slot takes next
+  unsigned error;                                      // a bounded wait inside the workgroup gave up
+};
+
+// Pairs [begin, end) of workgroup g in a projection of P pairs.
+__device__ __forceinline__ int range_begin(int P, int G, int g) { return (int)(((long long)P * g) / G); }
+
+// Walks one compute wave's weight-tile sequence: projection, pair (unit,
+// segment), then within the pair k-tile jk (0, 1: k-tiles 2w, 2w+1 of the
+// segment) and row-block jr of the unit, jr fastest.  All counters advance
+// incrementally (no division per tile).
+struct Seq {
+  const SeqDesc* desc;  // LDS
+  int count, G, g;
+  int p;          // projection (count: finished)
+  int pair, end;  // current pair (index in p) and end of this workgroup's pairs
+  int begin;      // first pair of this workgroup in p
+  int unit, seg;  // pair = unit * NS + seg
+  int jk, jr;     // k-tile of the wave's two, row-block of the unit
+  int rbw, KT, NS;
+  const bf16x8_t* w;
+
+  __device__ __forceinline__ void enter(int from) {
+    for (p = from; p < count; ++p) {
+      const SeqDesc d = desc[p];
+      const int P = d.units * (d.KT / kSeg);
+      pair = range_begin(P, G, g);
+      end = range_begin(P, G, g + 1);
+      begin = pair;
+      if (pair < end) {
+        rbw = d.rbw;
+        KT = d.KT;
+        NS = d.KT / kSeg;
+        w = d.w;
+        unit = pair / NS;
+        seg = pair - unit * NS;
+        jk = 0;
+        jr = 0;
+        return;
       }
     }
-    const unsigned long long packed =
-        (unsigned long long)pack_bf16x2(v[0], v[1]) | ((unsigned long long)pack_bf16x2(v[2], v[3]) << 32);
-    coherent_store64(d.y + (size_t)m * d.ldy + n, packed);
   }
-  // Publish: the wave's output stores have completed (vmcnt counts stores on
-  // this target) before the item counter moves.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (lane == 0) __hip_atomic_fetch_add(done_p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __device__ __forceinline__ bool done() const { return p >= count; }
+  __device__ __forceinline__ void advance() {
+    if (++jr < rbw) return;
+    jr = 0;
+    if (++jk < kWaveTiles) return;
+    jk = 0;
+    if (++seg == NS) {
+      seg = 0;
+      ++unit;
+    }
+    if (++pair < end) return;
+    enter(p + 1);
+  }
+  // This lane's 16 bytes of the current tile for compute wave `wave`.
+  __device__ __forceinline__ const bf16x8_t* tile(int wave, int lane) const {
+    const int kt = seg * kSeg + kWaveTiles * wave + jk;
+    const int rb = unit * rbw + jr;
+    return w + ((size_t)rb * KT + kt) * 64 + lane;
+  }
+  __device__ __forceinline__ bool pair_first() const { return jk == 0 && jr == 0; }
+  __device__ __forceinline__ bool pair_last() const { return jk == kWaveTiles - 1 && jr == rbw - 1; }
+  // The current pair is the last of its unit inside this workgroup's range.
+  __device__ __forceinline__ bool range_last() const { return pair + 1 == end || seg + 1 == NS; }
+};
+
+// Weight ring of a compute wave.  The loads and their waits are explicit:
+// with the bookkeeping branches of a tile step between a slot's load and
+// its use, the compiler's own wait analysis falls back to vmcnt(0) and
+// drains the ring every tile.  A compute wave issues no other vector memory
+// operation, exactly one ring load per tile step, so "the oldest slot has
+// landed" is exactly vmcnt(kRing - 1).  The wait names the slot's registers
+// as in/out operands, so the multiply that reads them cannot be scheduled
+// above it.
+__device__ __forceinline__ void ring_load(bf16x8_t& dst, const bf16x8_t* p) {
+  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(dst) : "v"(p) : "memory");
+}
+__device__ __forceinline__ void ring_wait(bf16x8_t& slot) {
+  static_assert(kRing == 16, "the wait count below is kRing - 1");
+  asm volatile("s_waitcnt vmcnt(15)" : "+v"(slot) : : "memory");
 }
 
-// Wave 0: wait until projection `dep` has published all of its items.
-// Once any wait of the launch has given up, later waits return at once, so a
-// broken program ends in about one spin limit rather than one per projection.
-__device__ __forceinline__ void wait_projection(unsigned* done_dep, unsigned target, unsigned* error) {
-  unsigned spins = 0;
-  while (__hip_atomic_load(done_dep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-    if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-    __builtin_amdgcn_s_sleep(2);
-    if (++spins > kSpinLimit) {
-      __hip_atomic_store(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
+// ------------------------------------------------------------ compute waves
+__device__ __forceinline__ void compute_wave(const StackProgram* prog, Shared& sh, unsigned* ws, int wave, int lane) {
+  Seq con{sh.seq, prog->count, (int)gridDim.x, (int)blockIdx.x};
+  con.enter(0);
+  Seq iss = con;
+  const bf16x8_t* dummy = prog->desc[0].w + lane;  // any valid address, for loads past the end
+
+  bf16x8_t ring[kRing];
+#pragma unroll
+  for (int k = 0; k < kRing; ++k) {
+    ring_load(ring[k], iss.done() ? dummy : iss.tile(wave, lane));
+    if (!iss.done()) iss.advance();
+  }
+
+  // Activation fragment: token (column) lane & 15, K chunk lane >> 4; the
+  // tokens >= M of the 16 MFMA columns are zero (read row 0, then masked).
+  const int M = prog->M;
+  const int nslots = x_slots(M);
+  const int slot_bytes = M * kXRow;
+  const bool x_valid = (lane & 15) < M;
+  const int x_lane = (x_valid ? (lane & 15) : 0) * kXRow + (lane >> 4) * 16 + kWaveTiles * wave * (kTileK * 2);
+  const unsigned x_keep = x_valid ? ~0u : 0u;
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  bf16x8_t xf0 = {}, xf1 = {};
+  unsigned pair_seq = 0, range_seq = 0;
+
+  // One tile: multiply ring slot k (a compile-time index, so the ring stays
+  // in registers), refill it, and do the pair / unit-range bookkeeping.
+  // Every step issues exactly one weight load (past the end of the sequence
+  // a valid dummy address), which keeps ring_wait's count exact.
+  auto tile = [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    ring_wait(ring[k]);
+    if (!con.done()) {
+      if (con.pair_first()) {
+        const int slot = pair_seq % nslots;
+        unsigned spins = 0;
+        while (lds_load(&sh.x_ready[slot]) != pair_seq + 1 && lds_load(&sh.error) == 0u) {
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins > kSpinLimit) {
+            lds_store(&sh.error, 1u + (pair_seq << 8));
+            break;
+          }
+        }
+        asm volatile("" ::: "memory");
+        const unsigned char* xs = sh.xbuf + slot * slot_bytes + x_lane;
+        xf0 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(xs) & x_keep);
+        xf1 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(xs + kTileK * 2) & x_keep);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane == 0) lds_add(&sh.x_done[slot], 1u);  // one count per wave
+      }
+      if (wave == 0 && con.pair == con.begin && con.pair_first())
+        LSK_TRACE(ws, con.count, con.G, con.g, con.p, 2, lane);
+      if (wave == 0 && con.pair + 1 == con.end && con.pair_last())
+        LSK_TRACE(ws, con.count, con.G, con.g, con.p, 3, lane);
+      const bf16x8_t xf = con.jk ? xf1 : xf0;
+      if (con.jr == 0)
+        acc0 = mfma16(ring[k], xf, acc0);
+      else
+        acc1 = mfma16(ring[k], xf, acc1);
+      if (con.pair_last()) {
+        if (con.range_last()) {
+          const int rs = range_seq % kRedSlots;
+          unsigned spins = 0;
+          while (lds_load(&sh.red_next[rs]) != range_seq && lds_load(&sh.error) == 0u) {  // slot free for us
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins > kSpinLimit) {
+              lds_store(&sh.error, 3u + (range_seq << 8));
+              break;
+            }
+          }
+          asm volatile("" ::: "memory");
+          sh.red[rs][wave][0][lane] = acc0;
+          sh.red[rs][wave][1][lane] = acc1;
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          if (lane == 0) lds_add(&sh.red_count[rs], 1u);  // one count per wave
+          acc0 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          acc1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          ++range_seq;
+        }
+        ++pair_seq;
+      }
+      con.advance();
+    }
+    ring_load(ring[k], iss.done() ? dummy : iss.tile(wave, lane));
+    if (!iss.done()) iss.advance();
+  };
+  while (!con.done()) unroll<kRing>(tile);
+}
+
+// ------------------------------------------------------------- control wave
+struct ControlCtx {
+  const StackProgram* prog;
+  Shared* sh;
+  unsigned* ws;
+  unsigned* progress;   // G words
+  unsigned* flags;      // count x G words
+  unsigned char* parts; // count x G partial slots of kStackPartialBytes
+  int G, g, lane, M;
+};
+
+// The first bounded wait of a launch to give up claims the detail record
+// (workspace words kStackWsDetail..+7): workgroup + 1, which wait gave up,
+// and the control wave's cursors, for lsk_stack_error's caller to inspect.
+__device__ __forceinline__ void record_error(const ControlCtx& c, unsigned code, unsigned a = 0, unsigned b = 0,
+                                             unsigned d = 0, unsigned e = 0, unsigned f = 0) {
+  unsigned expected = 0u;
+  if (__hip_atomic_compare_exchange_strong((global_u32*)(c.ws + kStackWsDetail), &expected, (unsigned)c.g + 1u,
+                                           __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    const unsigned v[6] = {code, a, b, d, e, f};
+    for (int i = 0; i < 6; ++i) coherent_store32(c.ws + kStackWsDetail + 1 + i, v[i]);
+  }
+  coherent_store32(c.ws + kStackWsError, 1u);
+}
+
+// Have all workgroups completed projections 0..q?  (One poll, no wait.)
+__device__ __forceinline__ bool projections_done(const ControlCtx& c, int q) {
+  // Up to 4 * 64 workgroups per poll, all loads issued before the compares.
+  bool ok = true;
+  for (int base = 0; base < c.G; base += 4 * 64) {
+    unsigned v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = base + i * 64 + c.lane;
+      v[i] = coherent_load32(c.progress + (idx < c.G ? idx : c.G - 1));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ok &= v[i] > (unsigned)q;
+  }
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+
+// Epilogue of unit `unit` of projection d from the summed accumulators.
+// Lane l holds output rows 4(l>>4)+i (i < 4) of the unit for token l & 15.
+__device__ __forceinline__ void store_unit(const ControlCtx& c, const StackDesc& d, int unit, const f32x4_t& a0,
+                                           const f32x4_t& a1) {
+  const int m = c.lane & 15;
+  if (m >= c.M) return;
+  const int n = unit * kTileRows + 4 * (c.lane >> 4);  // output column (intermediate index for SiLU*up)
+  float v[4];
+  if (d.epi == static_cast<int>(Epilogue::kSiluMul)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = silu_mul_bf16(a0[i], a1[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = bf16_round(a0[i]);
+    if (d.epi == static_cast<int>(Epilogue::kResidualAdd)) {
+      const unsigned long long r = coherent_load64(d.res + (size_t)m * d.ldr + n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] += __builtin_bit_cast(float, (unsigned)((r >> (16 * i)) & 0xffffu) << 16);
     }
   }
-  asm volatile("" ::: "memory");  // keep the activation loads after the wait
+  const unsigned long long packed = (unsigned long long)bf16_bits(v[0]) | ((unsigned long long)bf16_bits(v[1]) << 16) |
+                                    ((unsigned long long)bf16_bits(v[2]) << 32) |
+                                    ((unsigned long long)bf16_bits(v[3]) << 48);
+  coherent_store64(d.y + (size_t)m * d.ldy + n, packed);
 }
 
-__global__ __launch_bounds__(kWaves * 64, 1) void decode_stack_kernel(const StackProgram* __restrict__ prog,
-                                                                       unsigned* __restrict__ ws) {
-  // Cross-wave reduction slots (dynamic LDS, two alternating item slots).
-  extern __shared__ f32x4_t lds_dyn[];
-  f32x4_t (*red)[kWaves - 1][2][64] = reinterpret_cast<f32x4_t (*)[kWaves - 1][2][64]>(lds_dyn);
-  __shared__ int s_dep_ok;
+__device__ __forceinline__ unsigned char* partial_slot(const ControlCtx& c, int p, int g) {
+  return c.parts + ((size_t)p * c.G + g) * kStackPartialBytes;
+}
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int M = prog->M;
-  if (prog->magic != kStackMagic) {
-    if (threadIdx.x == 0) __hip_atomic_store(ws + kStackWsError, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void store_partial(unsigned char* slot, int lane, const f32x4_t& v) {
+  unsigned long long* q = reinterpret_cast<unsigned long long*>(slot + lane * 16);
+  coherent_store64(q, (unsigned long long)__float_as_uint(v[0]) | ((unsigned long long)__float_as_uint(v[1]) << 32));
+  coherent_store64(q + 1, (unsigned long long)__float_as_uint(v[2]) | ((unsigned long long)__float_as_uint(v[3]) << 32));
+}
+
+__device__ __forceinline__ void add_partial(f32x4_t& v, const unsigned char* slot, int lane) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(slot + lane * 16);
+  const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
+  v[0] += __uint_as_float((unsigned)lo);
+  v[1] += __uint_as_float((unsigned)(lo >> 32));
+  v[2] += __uint_as_float((unsigned)hi);
+  v[3] += __uint_as_float((unsigned)(hi >> 32));
+}
+
+// Finish the unit range [pb, pe) of projection p (summed accumulators a0, a1).
+__device__ void finish_range(const ControlCtx& c, int p, int pb, int pe, f32x4_t a0, f32x4_t a1) {
+  const StackDesc& d = c.prog->desc[p];
+  const int NS = d.KT / kSeg;
+  const int P = d.units * NS;
+  const int unit = pb / NS;
+  const int unit_end = (unit + 1) * NS;
+  if (pb % NS != 0) {
+    // Entered mid-K: publish the partial for the owner (an earlier workgroup).
+    unsigned char* slot = partial_slot(c, p, c.g);
+    store_partial(slot, c.lane, a0);
+    if (d.rbw == 2) store_partial(slot + 1024, c.lane, a1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (c.lane == 0) coherent_store32(c.flags + (size_t)p * c.G + c.g, 1u);
     return;
   }
-  unsigned* done = ws + kStackWsCounters;
-  unsigned* error = ws + kStackWsError;
-  unsigned* exit_count = ws + kStackWsExit;
-
-  Ctx x{prog->desc, prog->count, prog->total_items, wave, lane};
-  if (threadIdx.x == 0) s_dep_ok = -1;  // highest projection whose input wait is done
-
-  Cursor cur;
-  open_item(cur, x, blockIdx.x, 0);
-  bf16x8_t buf0[kChunkTiles], buf1[kChunkTiles], xv[kChunkTiles];
-  f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
-  int red_slot = 0;
-  __syncthreads();
-
-  if (cur.gi < x.total) {
-    const StackDesc& d = x.desc[cur.p];
-    if (d.rbw == 1) issue_weights<1>(buf0, d, cur, lane); else issue_weights<2>(buf0, d, cur, lane);
-  }
-
-  // One pipeline step: compute chunk `cur` (weights in `mine`), having first
-  // issued the next chunk's weights into `other`.
-  auto step = [&](bf16x8_t (&mine)[kChunkTiles], bf16x8_t (&other)[kChunkTiles]) {
-    const StackDesc& d = x.desc[cur.p];
-    if (cur.first && d.dep > s_dep_ok) {
-      // Input comes from earlier projections: wave 0 acquires every
-      // projection up to d.dep, the other waves wait here with their weight
-      // loads in flight.
-      if (wave == 0) {
-        for (int q = s_dep_ok + 1; q <= d.dep; ++q) wait_projection(done + q, (unsigned)x.desc[q].items, error);
-        if (lane == 0) s_dep_ok = d.dep;
-      }
-      __syncthreads();
-    }
-    issue_x(xv, d, cur, M, lane);
-    Cursor nxt = cur;
-    advance(nxt, x);
-    if (nxt.gi < x.total) {
-      const StackDesc& dn = x.desc[nxt.p];
-      if (dn.rbw == 1) issue_weights<1>(other, dn, nxt, lane); else issue_weights<2>(other, dn, nxt, lane);
-    }
-    if (d.rbw == 1) consume<1>(acc, mine, xv, cur.nkt); else consume<2>(acc, mine, xv, cur.nkt);
-    if (is_last(cur)) {
-      // Reduce the item's 8 partial tiles in wave order (LDS slot alternates
-      // so wave 0 can still be reading the previous item's slot).
-      if (wave > 0) {
-        red[red_slot][wave - 1][0][lane] = acc[0];
-        red[red_slot][wave - 1][1][lane] = acc[1];
-      }
-      __syncthreads();
-      if (wave == 0) {
-#pragma unroll
-        for (int w = 0; w < kWaves - 1; ++w) {
-          acc[0] += red[red_slot][w][0][lane];
-          acc[1] += red[red_slot][w][1][lane];
+  // Owner: add the partials of the later workgroups that finish the unit.
+  for (int j = c.g + 1, covered = pe; covered < unit_end && j < c.G; ++j) {
+    const int jb = range_begin(P, c.G, j), je = range_begin(P, c.G, j + 1);
+    if (je > jb) {
+      unsigned* flag = c.flags + (size_t)p * c.G + j;
+      unsigned spins = 0;
+      while (coherent_load32(flag) == 0u && coherent_load32(c.ws + kStackWsError) == 0u) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins > kSpinLimit) {
+          record_error(c, 4u, (unsigned)p, (unsigned)j, (unsigned)pb, (unsigned)pe);
+          break;
         }
-        finish_item(d, cur.item, acc, M, lane, done + cur.p);
       }
-      red_slot ^= 1;
-      acc[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      acc[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      asm volatile("" ::: "memory");
+      const unsigned char* slot = partial_slot(c, p, j);
+      add_partial(a0, slot, c.lane);
+      if (d.rbw == 2) add_partial(a1, slot + 1024, c.lane);
+      if (c.lane == 0) coherent_store32(flag, 0u);
     }
-    cur = nxt;
+    covered = je;
+  }
+  store_unit(c, d, unit, a0, a1);
+}
+
+// A bounded wait of a control wave has gone on too long, or another wave or
+// workgroup gave up: record it once and release every wave of the workgroup.
+__device__ __forceinline__ bool give_up(const ControlCtx& c, unsigned& idle, unsigned code, unsigned a, unsigned b) {
+  if (++idle <= kIdleLimit && !((idle & 1023u) == 0u && (coherent_load32(c.ws + kStackWsError) != 0u ||
+                                                         lds_load(&c.sh->error) != 0u)))
+    return false;
+  const unsigned lerr = lds_load(&c.sh->error);
+  record_error(c, lerr != 0u ? (0x100u | lerr) : (idle > kIdleLimit ? code : 7u), a, b);
+  lds_store(&c.sh->error, 1u);
+  return true;
+}
+
+// Stager: activation segments of this workgroup's pairs, in pair order, into
+// the LDS slots.  A batch takes the next pairs whose slot is free and whose
+// dependency is met, up to kBatchRows activation rows (M per pair); all its
+// row loads are issued before the first is written to LDS, so a batch costs
+// one memory round trip.  (Plain coherent loads and LDS stores: an LDS DMA
+// anywhere in the kernel makes the compiler wait for all vector memory
+// before every LDS read, which would drain the compute waves' weight rings.)
+constexpr int kBatchRows = 16;
+
+struct XCursor {
+  int xp, xpair, xend, xbegin;
+  unsigned seq;
+};
+
+__device__ __forceinline__ void stager_wave(const ControlCtx& c) {
+  const StackProgram* prog = c.prog;
+  Shared& sh = *c.sh;
+  const int G = c.G, g = c.g, count = prog->count, M = c.M, lane = c.lane;
+  auto enter = [&](XCursor& x, int from) {
+    for (x.xp = from; x.xp < count; ++x.xp) {
+      const StackDesc& d = prog->desc[x.xp];
+      const int P = d.units * (d.KT / kSeg);
+      x.xpair = range_begin(P, G, g);
+      x.xend = range_begin(P, G, g + 1);
+      x.xbegin = x.xpair;
+      if (x.xpair < x.xend) return;
+    }
+  };
+  auto next_pair = [&](XCursor& x) {
+    ++x.seq;
+    if (++x.xpair >= x.xend) enter(x, x.xp + 1);
+  };
+  XCursor cur{0, 0, 0, 0, 0u};
+  enter(cur, 0);
+  unsigned idle = 0;
+  int dep_ok = -1;  // projections <= dep_ok are known complete everywhere
+  const int nslots = x_slots(M);
+  const int slot_bytes = M * kXRow;
+
+  // Row r of the batch that starts at cursor b: f(r, source, LDS destination).
+  auto walk = [&](const XCursor& b, int nrows, auto&& f) {
+    XCursor x = b;
+    int m = 0;
+    unroll<kBatchRows>([&](auto rc) {
+      constexpr int r = decltype(rc)::value;
+      if (r < nrows) {
+        const StackDesc& d = prog->desc[x.xp];
+        const int seg = x.xpair % (d.KT / kSeg);
+        f(IntC<r>{}, d.x + (size_t)m * d.ldx + (size_t)seg * kSeg * kTileK + 8 * lane,
+          sh.xbuf + (x.seq % nslots) * slot_bytes + m * kXRow + 16 * lane);
+        if (++m == M) {
+          m = 0;
+          next_pair(x);
+        }
+      }
+    });
   };
 
-  while (cur.gi < x.total) {
-    step(buf0, buf1);
-    if (cur.gi >= x.total) break;
-    step(buf1, buf0);
+  while (cur.xp < count) {
+    // Collect the batch.
+    const XCursor start = cur;
+    int nrows = 0;
+    while (cur.xp < count && nrows + M <= kBatchRows) {
+      const int slot = cur.seq % nslots;
+      if (!(cur.seq < (unsigned)nslots || lds_load(&sh.x_done[slot]) == (unsigned)kCompute)) break;
+      const StackDesc& d = prog->desc[cur.xp];
+      if (d.dep > dep_ok) {
+        if (!projections_done(c, d.dep)) break;
+        dep_ok = d.dep;
+        LSK_TRACE(c.ws, count, G, g, cur.xp, 0, lane);
+      }
+      nrows += M;
+      next_pair(cur);
+    }
+    if (nrows == 0) {
+      __builtin_amdgcn_s_sleep(1);
+      if (give_up(c, idle, 5u, (unsigned)cur.xp, cur.seq)) return;
+      continue;
+    }
+    idle = 0;
+    u32x4_t rows[kBatchRows];
+    walk(start, nrows, [&](auto rc, const __bf16* src, unsigned char*) {
+      const unsigned long long* q = reinterpret_cast<const unsigned long long*>(src);
+      const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
+      rows[decltype(rc)::value] = u32x4_t{(unsigned)lo, (unsigned)(lo >> 32), (unsigned)hi, (unsigned)(hi >> 32)};
+    });
+    walk(start, nrows, [&](auto rc, const __bf16*, unsigned char* dst) {
+      *reinterpret_cast<u32x4_t*>(dst) = rows[decltype(rc)::value];
+    });
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (unsigned q = start.seq; q < cur.seq; ++q) {
+      lds_store(&sh.x_done[q % nslots], 0u);
+      lds_store(&sh.x_ready[q % nslots], q + 1);
+    }
+    if (start.xpair == start.xbegin) LSK_TRACE(c.ws, count, G, g, start.xp, 1, lane);
+  }
+}
+
+// Finisher: the compute waves' partials of each unit range, in order, then
+// the range's epilogue or cross-workgroup partial, and this workgroup's
+// progress word after its last range of each projection.
+__device__ __forceinline__ void finisher_wave(const ControlCtx& c) {
+  const StackProgram* prog = c.prog;
+  Shared& sh = *c.sh;
+  const int G = c.G, g = c.g, count = prog->count, lane = c.lane;
+  int rp = 0, rb = 0, re = 0, rend = 0;
+  auto r_next_range = [&](int from_pair) {
+    // First unit range starting at pair from_pair of projection rp, or the next projection's first.
+    while (rp < count) {
+      const StackDesc& d = prog->desc[rp];
+      const int NS = d.KT / kSeg;
+      const int P = d.units * NS;
+      if (from_pair < 0) from_pair = range_begin(P, G, g);
+      rend = range_begin(P, G, g + 1);
+      if (from_pair < rend) {
+        rb = from_pair;
+        const int unit_end = (from_pair / NS + 1) * NS;
+        re = unit_end < rend ? unit_end : rend;
+        return;
+      }
+      ++rp;
+      from_pair = -1;
+    }
+  };
+  r_next_range(-1);
+  unsigned range_seq = 0, idle = 0;
+  int published = 0;  // projections whose progress this workgroup has published
+  while (rp < count || published < count) {
+    bool did = false;
+    if (rp < count) {
+      const int rs = range_seq % kRedSlots;
+      if (lds_load(&sh.red_count[rs]) == (unsigned)kCompute) {
+        asm volatile("" ::: "memory");
+        f32x4_t a0 = sh.red[rs][0][0][lane], a1 = sh.red[rs][0][1][lane];
+#pragma unroll
+        for (int w = 1; w < kCompute; ++w) {
+          a0 += sh.red[rs][w][0][lane];
+          a1 += sh.red[rs][w][1][lane];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        lds_store(&sh.red_count[rs], 0u);
+        lds_store(&sh.red_next[rs], range_seq + kRedSlots);
+        finish_range(c, rp, rb, re, a0, a1);
+        ++range_seq;
+        r_next_range(re);
+        did = true;
+      }
+    }
+    if (published < rp) {
+      LSK_TRACE(c.ws, count, G, g, rp - 1, 4, lane);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // outputs and partials stored
+      published = rp;
+      if (lane == 0) coherent_store32(c.progress + g, (unsigned)published);
+      LSK_TRACE(c.ws, count, G, g, rp - 1, 5, lane);
+      did = true;
+    }
+    if (did) {
+      idle = 0;
+    } else {
+      __builtin_amdgcn_s_sleep(1);
+      if (give_up(c, idle, 8u, (unsigned)rp | ((unsigned)published << 16), range_seq)) return;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(const StackProgram* __restrict__ prog,
+                                                                    unsigned* __restrict__ ws) {
+  __shared__ Shared sh;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (prog->magic != kStackMagic || prog->M < 1 || prog->M > kTileRows || prog->count > kStackMaxProjections) {
+    if (threadIdx.x == 0) coherent_store32(ws + kStackWsError, 2u);
+    return;
+  }
+  for (int i = threadIdx.x; i < prog->count; i += kThreads) {
+    const StackDesc& d = prog->desc[i];
+    sh.seq[i] = SeqDesc{d.w, d.units, (short)d.KT, (short)d.rbw};
+  }
+  if (threadIdx.x < kMaxXSlots) {
+    sh.x_ready[threadIdx.x] = 0u;
+    sh.x_done[threadIdx.x] = 0u;
+  }
+  if (threadIdx.x < kRedSlots) {
+    sh.red_count[threadIdx.x] = 0u;
+    sh.red_next[threadIdx.x] = threadIdx.x;
+  }
+  if (threadIdx.x == 0) sh.error = 0u;
+  __syncthreads();
+
+  if (wave < kCompute) {
+    compute_wave(prog, sh, ws, wave, lane);
+  } else {
+    ControlCtx c{prog, &sh, ws, ws + kStackWsProgress, ws + kStackWsFlags, nullptr, (int)gridDim.x,
+                 (int)blockIdx.x, lane, prog->M};
+    c.parts = reinterpret_cast<unsigned char*>(ws) + kStackWsPartialsOffset(prog->count, (int)gridDim.x);
+    if (wave == kCompute)
+      stager_wave(c);
+    else
+      finisher_wave(c);
   }
 
-  // Last workgroup out resets the counters for the next launch.
+  // Last workgroup out clears the progress words for the next launch.
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned old = __hip_atomic_fetch_add(exit_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned* exit_count = ws + kStackWsExit;
+    const unsigned old = __hip_atomic_fetch_add(exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == gridDim.x - 1) {
-      for (int p = 0; p < x.count; ++p) __hip_atomic_store(done + p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(exit_count, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < (int)gridDim.x; ++i) coherent_store32(ws + kStackWsProgress + i, 0u);
+      coherent_store32(exit_count, 0u);
     }
   }
 }
 
 }  // namespace
 
-size_t stack_lds_bytes() { return sizeof(f32x4_t) * 2 * (kWaves - 1) * 2 * 64; }
+size_t stack_lds_bytes() { return 0; }
 
 const void* stack_kernel_symbol() { return reinterpret_cast<const void*>(&decode_stack_kernel); }
 
+int stack_threads() { return kThreads; }
+
 hipError_t launch_decode_stack(const StackProgram* prog, unsigned* ws, int grid, size_t lds_bytes,
                                hipStream_t stream) {
-  decode_stack_kernel<<<dim3(grid), dim3(kWaves * 64), lds_bytes, stream>>>(prog, ws);
+  decode_stack_kernel<<<dim3(grid), dim3(kThreads), lds_bytes, stream>>>(prog, ws);
   return hipGetLastError();
 }
 

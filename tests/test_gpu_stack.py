@@ -91,25 +91,33 @@ def test_stack_dependency_chain_matches_oracle(gpu, m):
             assert_parity(got.cpu(), want, f"stack chain M={m} layer {l} {name}")
 
 
-def test_stack_matches_single_launches_bitwise(gpu):
-    """Projections whose standalone kernel splits K over 8 waves (qkv, o,
-    gate_up) give bitwise-identical outputs in the persistent kernel."""
+def test_stack_independent_projections_and_determinism(gpu):
+    """Independent projections (no dependencies) match the oracle, and two
+    launches of one program give bitwise-identical outputs (fixed summation
+    order: compute waves, then workgroups in index order)."""
     m = 3
     w = _layer_weights(5)
     p = _packed(w)
-    xs = [activations(m, k, seed=20 + i).to(DEV) for i, k in enumerate((G.hidden_size, G.q_dim, G.hidden_size))]
-    y_single = [kernels.linear(xs[0], p["qkv"]), kernels.linear(xs[1], p["o"]),
-                kernels.linear(xs[2], p["gate_up"], epilogue=_lib.EPI_SILU_MUL)]
-    outs = [torch.empty_like(y) for y in y_single]
+    xs = [activations(m, k, seed=20 + i) for i, k in enumerate((G.hidden_size, G.q_dim, G.hidden_size))]
+    outs = [torch.full((m, n), float("nan"), device=DEV, dtype=torch.bfloat16)
+            for n in (G.qkv_dim, G.hidden_size, G.intermediate_size)]
     specs = [
-        {"x": xs[0], "weight": p["qkv"], "out": outs[0]},
-        {"x": xs[1], "weight": p["o"], "out": outs[1]},
-        {"x": xs[2], "weight": p["gate_up"], "out": outs[2], "epilogue": _lib.EPI_SILU_MUL},
+        {"x": xs[0].to(DEV), "weight": p["qkv"], "out": outs[0]},
+        {"x": xs[1].to(DEV), "weight": p["o"], "out": outs[1]},
+        {"x": xs[2].to(DEV), "weight": p["gate_up"], "out": outs[2], "epilogue": _lib.EPI_SILU_MUL},
     ]
     step = kernels.StackStep(specs, m, DEV)
     step.launch()
     assert step.error() == 0
-    for a, b in zip(outs, y_single):
+    first = [o.clone() for o in outs]
+    assert_parity(outs[0].cpu(), ref.linear(xs[0], w["qkv"]), "stack qkv")
+    assert_parity(outs[1].cpu(), ref.linear(xs[1], w["o"]), "stack o")
+    assert_parity(outs[2].cpu(), ref.silu_mul(ref.linear(xs[2], w["gate_up"]), G.intermediate_size), "stack gate_up")
+    for o in outs:
+        o.fill_(float("nan"))
+    step.launch()
+    assert step.error() == 0
+    for a, b in zip(outs, first):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
@@ -143,11 +151,17 @@ def test_stack_graph_replays(gpu):
         for got, want in zip(bufs[-1], eager):
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {replay} differs"
     assert step.error() == 0
-    assert int(step.workspace.view(torch.int32)[_lib_counters_offset():].abs().sum()) == 0
+    assert _sync_words_clear(step)
 
 
-def _lib_counters_offset() -> int:
-    return 16  # kStackWsCounters: done[] counters start at word 16
+def _sync_words_clear(step) -> bool:
+    """Exit counter, per-workgroup progress words and per-(projection,
+    workgroup) partial flags are all back to zero (workspace words 1,
+    64 .. 64+G and 2048 .. 2048+count*G)."""
+    grid = torch.cuda.get_device_properties(0).multi_processor_count
+    words = step.workspace.view(torch.int32)
+    return (int(words[1]) == 0 and int(words[64:64 + grid].abs().sum()) == 0
+            and int(words[2048:2048 + step.count * grid].abs().sum()) == 0)
 
 
 def test_stack_rejects_bad_programs(gpu):
@@ -160,7 +174,7 @@ def test_stack_rejects_bad_programs(gpu):
         kernels.StackStep([{"x": torch.zeros((17, G.hidden_size), device=DEV, dtype=torch.bfloat16),
                             "weight": w["qkv"], "out": torch.empty((17, G.qkv_dim), device=DEV,
                                                                    dtype=torch.bfloat16)}], 17, DEV)
-    small = PackedWeight.from_rowmajor(weight(64, 128, seed=3).to(DEV))  # K/32 = 4 < 8 waves
+    small = PackedWeight.from_rowmajor(weight(64, 128, seed=3).to(DEV))  # K = 128, not a multiple of 512
     with pytest.raises(ValueError):
         kernels.StackStep([{"x": torch.zeros((1, 128), device=DEV, dtype=torch.bfloat16), "weight": small,
                             "out": torch.empty((1, 64), device=DEV, dtype=torch.bfloat16)}], 1, DEV)
