@@ -132,15 +132,26 @@ __device__ __forceinline__ void coherent_store32(unsigned* p, unsigned v) {
                                        ((size_t)(g_) * (count_) + (p_)) * 8 + (ev_)),                             \
                          (unsigned)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); \
   } while (0)
+// Per compute wave: cycles in the ring wait, the activation wait, the
+// partial-slot wait, and in total, at word (G*count*8) + (g*8 + wave)*4 + i.
+#define LSK_STALL_BEGIN() const unsigned long long stall_t0_ = __builtin_amdgcn_s_memtime()
+#define LSK_STALL_END(acc_) (acc_) += __builtin_amdgcn_s_memtime() - stall_t0_
 #else
 #define LSK_TRACE(ws_, count_, G_, g_, p_, ev_, lane_) \
   do {                                                 \
+  } while (0)
+#define LSK_STALL_BEGIN() \
+  do {                    \
+  } while (0)
+#define LSK_STALL_END(acc_) \
+  do {                      \
   } while (0)
 #endif
 
 // Wave-uniform copy of a value the compiler cannot prove uniform (an LDS
 // load) but that is, so branches on it stay scalar.
 __device__ __forceinline__ unsigned uni(unsigned v) { return (unsigned)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // LDS words shared by the waves (relaxed workgroup-scope atomics: ds ops of
 // one wave execute in order, so flag/data ordering only needs the writer's
@@ -150,9 +161,6 @@ __device__ __forceinline__ unsigned lds_load(const unsigned* p) {
 }
 __device__ __forceinline__ void lds_store(unsigned* p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ __forceinline__ void lds_add(unsigned* p, unsigned v) {
-  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Activation slot i holds the M rows of one pair's segment at
@@ -173,181 +181,263 @@ struct SeqDesc {
 struct Shared {
   SeqDesc seq[kStackMaxProjections];
   unsigned char xbuf[kXBytes];                         // staged activation segments
+  unsigned char xzero[kXRow];                          // zeros: the fragment of tokens >= M
   f32x4_t red[kRedSlots][kCompute][2][64];             // compute-wave partials of a unit range
-  unsigned x_ready[kMaxXSlots];                        // pair sequence number + 1 of the slot's content
-  unsigned x_done[kMaxXSlots];                         // compute waves done reading the slot
-  unsigned red_count[kRedSlots];                       // compute waves that wrote the slot
-  unsigned red_next[kRedSlots];                        // unit-range number the slot takes next
+  unsigned x_staged;                                   // pairs whose activations are in their slot
+  unsigned x_used[kCompute];                           // pairs each compute wave has read
+  unsigned red_done[kCompute];                         // unit ranges each compute wave has written
+  unsigned red_freed;                                  // unit ranges the finisher has read
   unsigned error;                                      // a bounded wait inside the workgroup gave up
 };
 
 // Pairs [begin, end) of workgroup g in a projection of P pairs.
-__device__ __forceinline__ int range_begin(int P, int G, int g) { return (int)(((long long)P * g) / G); }
+// (P * G < 2^32: packed weights are under 4 GiB and G <= kStackMaxGrid.)
+__device__ __forceinline__ int range_begin(int P, int G, int g) { return (int)((unsigned)P * (unsigned)g / (unsigned)G); }
 
-// Walks one compute wave's weight-tile sequence: projection, pair (unit,
-// segment), then within the pair k-tile jk (0, 1: k-tiles 2w, 2w+1 of the
-// segment) and row-block jr of the unit, jr fastest.  All counters advance
-// incrementally (no division per tile).
-struct Seq {
+// Raw buffer resource over `bytes` bytes at `base` (wave-uniform).
+constexpr int kNonTemporal = 2;  // buffer-load cache policy: streamed once
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)0x00020000u);
+}
+
+// A compute wave's weight-tile stream, one ring round (kRing tiles) at a
+// time.  Per projection it is the wave's tiles of the workgroup's pairs in
+// order (a pair: k-tiles jk = 0, 1 of the wave in one segment of a unit, for
+// each row-block jr of the unit, jr fastest), padded with dummy tiles (tile 0
+// of the projection, never multiplied) to whole rounds, so every projection
+// starts at ring slot 0.  next() returns one round: lane t < kRing holds the
+// byte offset of the round's tile t, and the resource of its projection.
+// The lanes compute the offsets in parallel, once per round; the tile steps
+// only read them.
+struct Round {
+  unsigned off;
+  __amdgpu_buffer_rsrc_t rsrc;
+};
+
+// Pairs [b, e) of workgroup g in projection d (0 pairs: b == e).
+struct Share {
+  int b, e, R, NS, KT;
+  __device__ __forceinline__ Share(const SeqDesc& d, int G, int g) {
+    KT = uni((int)d.KT);
+    NS = KT / kSeg;
+    R = uni((int)d.rbw);
+    const unsigned P = (unsigned)uni(d.units) * (unsigned)NS;
+    b = (int)(P * (unsigned)g / (unsigned)G);
+    e = (int)(P * (unsigned)(g + 1) / (unsigned)G);
+  }
+};
+
+struct Planner {
   const SeqDesc* desc;  // LDS
-  int count, G, g;
-  int p;          // projection (count: finished)
-  int pair, end;  // current pair (index in p) and end of this workgroup's pairs
-  int begin;      // first pair of this workgroup in p
-  int unit, seg;  // pair = unit * NS + seg
-  int jk, jr;     // k-tile of the wave's two, row-block of the unit
-  int rbw, KT, NS;
-  const bf16x8_t* w;
+  int count, G, g, wave, lane;
+  int p;                 // projection being issued; count: past the end (dummies)
+  int round, rounds, b, pairs, R, NS, KT;
+  __amdgpu_buffer_rsrc_t rsrc;
 
   __device__ __forceinline__ void enter(int from) {
     for (p = from; p < count; ++p) {
       const SeqDesc d = desc[p];
-      const int P = d.units * (d.KT / kSeg);
-      pair = range_begin(P, G, g);
-      end = range_begin(P, G, g + 1);
-      begin = pair;
-      if (pair < end) {
-        rbw = d.rbw;
-        KT = d.KT;
-        NS = d.KT / kSeg;
-        w = d.w;
-        unit = pair / NS;
-        seg = pair - unit * NS;
-        jk = 0;
-        jr = 0;
+      const Share s(d, G, g);
+      if (s.b < s.e) {
+        R = s.R;
+        KT = s.KT;
+        NS = s.NS;
+        b = s.b;
+        pairs = s.e - s.b;
+        rounds = (pairs * 2 * R + kRing - 1) / kRing;
+        round = 0;
+        rsrc = weight_rsrc(d.w, (unsigned)uni(d.units) * (unsigned)(R * KT) * 1024u);
         return;
       }
     }
   }
-  __device__ __forceinline__ bool done() const { return p >= count; }
-  __device__ __forceinline__ void advance() {
-    if (++jr < rbw) return;
-    jr = 0;
-    if (++jk < kWaveTiles) return;
-    jk = 0;
-    if (++seg == NS) {
-      seg = 0;
-      ++unit;
+  __device__ __forceinline__ Round next() {
+    Round r{0u, rsrc};
+    if (p < count) {
+      const int T = round * kRing + (lane & (kRing - 1));
+      const int pair = T >> R;  // 2R tiles per pair, R = 1 or 2
+      const int j = T & (2 * R - 1);
+      const int jr = j & (R - 1), jk = j >> (R - 1);
+      if (pair < pairs) {
+        const unsigned P = (unsigned)(b + pair);
+        const unsigned unit = P / (unsigned)NS;
+        const unsigned seg = P - unit * (unsigned)NS;
+        r.off = ((unit * R + jr) * (unsigned)KT + seg * kSeg + kWaveTiles * wave + jk) * 1024u;
+      }
+      if (++round == rounds) enter(p + 1);
     }
-    if (++pair < end) return;
-    enter(p + 1);
+    return r;
   }
-  // This lane's 16 bytes of the current tile for compute wave `wave`.
-  __device__ __forceinline__ const bf16x8_t* tile(int wave, int lane) const {
-    const int kt = seg * kSeg + kWaveTiles * wave + jk;
-    const int rb = unit * rbw + jr;
-    return w + ((size_t)rb * KT + kt) * 64 + lane;
-  }
-  __device__ __forceinline__ bool pair_first() const { return jk == 0 && jr == 0; }
-  __device__ __forceinline__ bool pair_last() const { return jk == kWaveTiles - 1 && jr == rbw - 1; }
-  // The current pair is the last of its unit inside this workgroup's range.
-  __device__ __forceinline__ bool range_last() const { return pair + 1 == end || seg + 1 == NS; }
 };
 
-// Weight ring of a compute wave.  The loads and their waits are explicit:
-// with the bookkeeping branches of a tile step between a slot's load and
-// its use, the compiler's own wait analysis falls back to vmcnt(0) and
-// drains the ring every tile.  A compute wave issues no other vector memory
-// operation, exactly one ring load per tile step, so "the oldest slot has
-// landed" is exactly vmcnt(kRing - 1).  The wait names the slot's registers
-// as in/out operands, so the multiply that reads them cannot be scheduled
-// above it.
-__device__ __forceinline__ void ring_load(bf16x8_t& dst, const bf16x8_t* p) {
-  asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(dst) : "v"(p) : "memory");
-}
-__device__ __forceinline__ void ring_wait(bf16x8_t& slot) {
-  static_assert(kRing == 16, "the wait count below is kRing - 1");
-  asm volatile("s_waitcnt vmcnt(15)" : "+v"(slot) : : "memory");
+__device__ __forceinline__ bf16x8_t ring_load(const Round& r, int k, unsigned lane16) {
+  return __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                          r.rsrc, lane16, (unsigned)__builtin_amdgcn_readlane((int)r.off, k),
+                                          kNonTemporal));
 }
 
 // ------------------------------------------------------------ compute waves
+// Each round multiplies the kRing tiles in the ring and refills every slot
+// with the planner's next round, so kRing tile loads stay in flight.  One
+// loop serves every projection (the row-block count R only selects which
+// accumulator and fragment a slot's multiply uses), so the ring keeps one
+// register assignment throughout.
 __device__ __forceinline__ void compute_wave(const StackProgram* prog, Shared& sh, unsigned* ws, int wave, int lane) {
-  Seq con{sh.seq, prog->count, (int)gridDim.x, (int)blockIdx.x};
-  con.enter(0);
-  Seq iss = con;
-  const bf16x8_t* dummy = prog->desc[0].w + lane;  // any valid address, for loads past the end
+  const int count = prog->count, G = gridDim.x, g = blockIdx.x;
+  Planner plan{sh.seq, count, G, g, wave, lane};
+  plan.rsrc = weight_rsrc(sh.seq[0].w, 1024u);
+  plan.enter(0);
+  const unsigned lane16 = (unsigned)lane * 16u;
 
   bf16x8_t ring[kRing];
-#pragma unroll
-  for (int k = 0; k < kRing; ++k) {
-    ring_load(ring[k], iss.done() ? dummy : iss.tile(wave, lane));
-    if (!iss.done()) iss.advance();
+  {
+    const Round r0 = plan.next();
+    unroll<kRing>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      ring[k] = ring_load(r0, k, lane16);
+    });
   }
 
-  // Activation fragment: token (column) lane & 15, K chunk lane >> 4; the
-  // tokens >= M of the 16 MFMA columns are zero (read row 0, then masked).
+  // Activation fragment: token (column) lane & 15, K chunk lane >> 4.  Lanes
+  // of tokens >= M read a zero row instead.
   const int M = prog->M;
   const int nslots = x_slots(M);
-  const int slot_bytes = M * kXRow;
+  const unsigned slot_bytes = (unsigned)(M * kXRow);
   const bool x_valid = (lane & 15) < M;
-  const int x_lane = (x_valid ? (lane & 15) : 0) * kXRow + (lane >> 4) * 16 + kWaveTiles * wave * (kTileK * 2);
-  const unsigned x_keep = x_valid ? ~0u : 0u;
+  const unsigned x_col = (unsigned)((lane >> 4) * 16 + kWaveTiles * wave * (kTileK * 2));
+  const unsigned x_lane = (unsigned)(uintptr_t)sh.xbuf + (unsigned)((lane & 15) * kXRow) + x_col;
+  const unsigned x_zero = (unsigned)(uintptr_t)sh.xzero + x_col;
+  unsigned pair_seq = 0, range_seq = 0;
+  unsigned x_avail = 0, red_avail = kRedSlots;  // pairs staged, unit ranges with a free slot (as last seen)
+  int slot = 0;
+  unsigned slot_off = 0;
+#ifdef LSK_STACK_TRACE
+  unsigned long long st_x = 0, st_red = 0;
+  const unsigned long long st_start = __builtin_amdgcn_s_memtime();
+#endif
+
+  // Consumer cursor: projection cp, its pairs, the pair done next, its segment.
+  int cp = -1, R = 1, NS = 1, pairs = 0, done = 0, seg = 0, rounds = 0, round = 0;
+  auto consume_enter = [&]() {
+    for (++cp; cp < count; ++cp) {
+      const Share s(sh.seq[cp], G, g);
+      if (s.b < s.e) {
+        R = s.R;
+        NS = s.NS;
+        pairs = s.e - s.b;
+        seg = s.b % s.NS;
+        done = 0;
+        rounds = (pairs * 2 * R + kRing - 1) / kRing;
+        round = 0;
+        return;
+      }
+    }
+  };
+  consume_enter();
+
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   bf16x8_t xf0 = {}, xf1 = {};
-  unsigned pair_seq = 0, range_seq = 0;
-
-  // One tile: multiply ring slot k (a compile-time index, so the ring stays
-  // in registers), refill it, and do the pair / unit-range bookkeeping.
-  // Every step issues exactly one weight load (past the end of the sequence
-  // a valid dummy address), which keeps ring_wait's count exact.
-  auto tile = [&](auto kc) {
-    constexpr int k = decltype(kc)::value;
-    ring_wait(ring[k]);
-    if (!con.done()) {
-      if (con.pair_first()) {
-        const int slot = pair_seq % nslots;
-        unsigned spins = 0;
-        while (lds_load(&sh.x_ready[slot]) != pair_seq + 1 && lds_load(&sh.error) == 0u) {
-          __builtin_amdgcn_s_sleep(1);
-          if (++spins > kSpinLimit) {
-            lds_store(&sh.error, 1u + (pair_seq << 8));
-            break;
-          }
-        }
-        asm volatile("" ::: "memory");
-        const unsigned char* xs = sh.xbuf + slot * slot_bytes + x_lane;
-        xf0 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(xs) & x_keep);
-        xf1 = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4_t*>(xs + kTileK * 2) & x_keep);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (lane == 0) lds_add(&sh.x_done[slot], 1u);  // one count per wave
-      }
-      if (wave == 0 && con.pair == con.begin && con.pair_first())
-        LSK_TRACE(ws, con.count, con.G, con.g, con.p, 2, lane);
-      if (wave == 0 && con.pair + 1 == con.end && con.pair_last())
-        LSK_TRACE(ws, con.count, con.G, con.g, con.p, 3, lane);
-      const bf16x8_t xf = con.jk ? xf1 : xf0;
-      if (con.jr == 0)
-        acc0 = mfma16(ring[k], xf, acc0);
-      else
-        acc1 = mfma16(ring[k], xf, acc1);
-      if (con.pair_last()) {
-        if (con.range_last()) {
-          const int rs = range_seq % kRedSlots;
-          unsigned spins = 0;
-          while (lds_load(&sh.red_next[rs]) != range_seq && lds_load(&sh.error) == 0u) {  // slot free for us
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins > kSpinLimit) {
-              lds_store(&sh.error, 3u + (range_seq << 8));
-              break;
+  bool real = false;
+  while (cp < count) {
+    const Round nr = plan.next();
+    const bool r2 = R == 2;
+    unroll<kRing>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      if constexpr (k % 2 == 0) {
+        if (!r2 || k % 4 == 0) {  // a pair starts: its activation fragments
+          real = done < pairs;
+          if (real) {
+            if (pair_seq >= x_avail) {
+              unsigned spins = 0;
+              LSK_STALL_BEGIN();
+#pragma clang loop unroll(disable)
+              while ((x_avail = lds_load(&sh.x_staged)) <= pair_seq) {
+                if (lds_load(&sh.error) != 0u) break;
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > kSpinLimit) {
+                  lds_store(&sh.error, 1u + (pair_seq << 8));
+                  break;
+                }
+              }
+              LSK_STALL_END(st_x);
             }
+            asm volatile("" ::: "memory");
+            const unsigned xa = x_valid ? x_lane + slot_off : x_zero;
+            const auto* xs = reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(xa);
+            xf0 = __builtin_bit_cast(bf16x8_t, xs[0]);
+            xf1 = __builtin_bit_cast(bf16x8_t, xs[kTileK * 2 / 16]);
+            // The LDS executes one wave's operations in order, so the stager
+            // (which reuses the slot only after seeing this count) cannot
+            // overwrite the fragments before these reads have taken them.
+            asm volatile("" ::: "memory");
+            lds_store(&sh.x_used[wave], pair_seq + 1);
+            if (wave == 0 && done == 0) LSK_TRACE(ws, count, G, g, cp, 2, lane);
           }
-          asm volatile("" ::: "memory");
-          sh.red[rs][wave][0][lane] = acc0;
-          sh.red[rs][wave][1][lane] = acc1;
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          if (lane == 0) lds_add(&sh.red_count[rs], 1u);  // one count per wave
-          acc0 = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          acc1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
-          ++range_seq;
         }
-        ++pair_seq;
       }
-      con.advance();
-    }
-    ring_load(ring[k], iss.done() ? dummy : iss.tile(wave, lane));
-    if (!iss.done()) iss.advance();
-  };
-  while (!con.done()) unroll<kRing>(tile);
+      if (real) {
+        if (r2) {  // tiles (jr, jk) = (k & 1, (k >> 1) & 1) of the pair
+          if constexpr (k % 2 == 0)
+            acc0 = mfma16(ring[k], ((k >> 1) & 1) ? xf1 : xf0, acc0);
+          else
+            acc1 = mfma16(ring[k], ((k >> 1) & 1) ? xf1 : xf0, acc1);
+        } else {  // tiles jk = k & 1 of one row-block
+          acc0 = mfma16(ring[k], (k & 1) ? xf1 : xf0, acc0);
+        }
+      }
+      ring[k] = ring_load(nr, k, lane16);
+      if constexpr (k % 2 == 1) {
+        if ((!r2 || k % 4 == 3) && real) {  // a pair ends
+          if (done + 1 == pairs || seg + 1 == NS) {  // ... and with it a unit range of this workgroup
+            if (wave == 0 && done + 1 == pairs) LSK_TRACE(ws, count, G, g, cp, 3, lane);
+            const int rs = range_seq % kRedSlots;
+            if (range_seq >= red_avail) {  // slot rs still holds range range_seq - kRedSlots
+              unsigned spins = 0;
+              LSK_STALL_BEGIN();
+#pragma clang loop unroll(disable)
+              while ((red_avail = lds_load(&sh.red_freed) + kRedSlots) <= range_seq) {
+                if (lds_load(&sh.error) != 0u) break;
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins > kSpinLimit) {
+                  lds_store(&sh.error, 3u + (range_seq << 8));
+                  break;
+                }
+              }
+              LSK_STALL_END(st_red);
+            }
+            asm volatile("" ::: "memory");
+            sh.red[rs][wave][0][lane] = acc0;
+            sh.red[rs][wave][1][lane] = acc1;
+            asm volatile("" ::: "memory");
+            lds_store(&sh.red_done[wave], range_seq + 1);  // after the partials, in LDS order
+            acc0 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            acc1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            ++range_seq;
+          }
+          ++pair_seq;
+          ++done;
+          if (++seg == NS) seg = 0;
+          slot_off += slot_bytes;
+          if (++slot == nslots) {
+            slot = 0;
+            slot_off = 0;
+          }
+        }
+      }
+    });
+    if (++round == rounds) consume_enter();
+  }
+#ifdef LSK_STACK_TRACE
+  if (lane == 0) {
+    unsigned* st = ws + kStackWsBytes(count, G) / 4 + (size_t)G * count * 8 + (g * 8 + wave) * 4;
+    const unsigned long long total = __builtin_amdgcn_s_memtime() - st_start;
+    st[0] = 0u;
+    st[1] = (unsigned)(st_x >> 8);
+    st[2] = (unsigned)(st_red >> 8);
+    st[3] = (unsigned)(total >> 8);
+  }
+#endif
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last round's (dummy) loads
 }
 
 // ------------------------------------------------------------- control wave
@@ -527,6 +617,17 @@ __device__ __forceinline__ void stager_wave(const ControlCtx& c) {
   int dep_ok = -1;  // projections <= dep_ok are known complete everywhere
   const int nslots = x_slots(M);
   const int slot_bytes = M * kXRow;
+  // Pairs every compute wave has read.
+  auto used_min = [&]() {
+    unsigned v[kCompute];
+#pragma unroll
+    for (int w = 0; w < kCompute; ++w) v[w] = __hip_atomic_load(&sh.x_used[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    unsigned m = v[0];
+#pragma unroll
+    for (int w = 1; w < kCompute; ++w) m = v[w] < m ? v[w] : m;
+    return uni(m);
+  };
+  unsigned used = 0;
 
   // Row r of the batch that starts at cursor b: f(r, source, LDS destination).
   auto walk = [&](const XCursor& b, int nrows, auto&& f) {
@@ -538,7 +639,7 @@ __device__ __forceinline__ void stager_wave(const ControlCtx& c) {
         const StackDesc& d = prog->desc[x.xp];
         const int seg = x.xpair % (d.KT / kSeg);
         f(IntC<r>{}, d.x + (size_t)m * d.ldx + (size_t)seg * kSeg * kTileK + 8 * lane,
-          sh.xbuf + (x.seq % nslots) * slot_bytes + m * kXRow + 16 * lane);
+          sh.xbuf + (x.seq % nslots) * slot_bytes + m * kXRow + 16 * lane, d.dep >= 0);
         if (++m == M) {
           m = 0;
           next_pair(x);
@@ -552,8 +653,10 @@ __device__ __forceinline__ void stager_wave(const ControlCtx& c) {
     const XCursor start = cur;
     int nrows = 0;
     while (cur.xp < count && nrows + M <= kBatchRows) {
-      const int slot = cur.seq % nslots;
-      if (!(cur.seq < (unsigned)nslots || lds_load(&sh.x_done[slot]) == (unsigned)kCompute)) break;
+      if (cur.seq >= used + (unsigned)nslots) {  // the slot's previous pair may still be read
+        used = used_min();
+        if (cur.seq >= used + (unsigned)nslots) break;
+      }
       const StackDesc& d = prog->desc[cur.xp];
       if (d.dep > dep_ok) {
         if (!projections_done(c, d.dep)) break;
@@ -570,19 +673,23 @@ __device__ __forceinline__ void stager_wave(const ControlCtx& c) {
     }
     idle = 0;
     u32x4_t rows[kBatchRows];
-    walk(start, nrows, [&](auto rc, const __bf16* src, unsigned char*) {
-      const unsigned long long* q = reinterpret_cast<const unsigned long long*>(src);
-      const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
-      rows[decltype(rc)::value] = u32x4_t{(unsigned)lo, (unsigned)(lo >> 32), (unsigned)hi, (unsigned)(hi >> 32)};
+    // Inputs ready at launch (no dependency) are not written by the program,
+    // so plain cacheable loads see them (and the XCD's L2 serves the other
+    // workgroups); inputs the program produces need device-coherent loads.
+    walk(start, nrows, [&](auto rc, const __bf16* src, unsigned char*, bool coherent) {
+      if (coherent) {
+        const unsigned long long* q = reinterpret_cast<const unsigned long long*>(src);
+        const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
+        rows[decltype(rc)::value] = u32x4_t{(unsigned)lo, (unsigned)(lo >> 32), (unsigned)hi, (unsigned)(hi >> 32)};
+      } else {
+        rows[decltype(rc)::value] = *reinterpret_cast<const u32x4_t*>(src);
+      }
     });
-    walk(start, nrows, [&](auto rc, const __bf16*, unsigned char* dst) {
+    walk(start, nrows, [&](auto rc, const __bf16*, unsigned char* dst, bool) {
       *reinterpret_cast<u32x4_t*>(dst) = rows[decltype(rc)::value];
     });
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    for (unsigned q = start.seq; q < cur.seq; ++q) {
-      lds_store(&sh.x_done[q % nslots], 0u);
-      lds_store(&sh.x_ready[q % nslots], q + 1);
-    }
+    lds_store(&sh.x_staged, cur.seq);
     if (start.xpair == start.xbegin) LSK_TRACE(c.ws, count, G, g, start.xp, 1, lane);
   }
 }
@@ -615,12 +722,25 @@ __device__ __forceinline__ void finisher_wave(const ControlCtx& c) {
   };
   r_next_range(-1);
   unsigned range_seq = 0, idle = 0;
+  // Unit ranges every compute wave has written.
+  auto written_min = [&]() {
+    unsigned v[kCompute];
+#pragma unroll
+    for (int w = 0; w < kCompute; ++w)
+      v[w] = __hip_atomic_load(&sh.red_done[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    unsigned m = v[0];
+#pragma unroll
+    for (int w = 1; w < kCompute; ++w) m = v[w] < m ? v[w] : m;
+    return uni(m);
+  };
+  unsigned written = 0;
   int published = 0;  // projections whose progress this workgroup has published
   while (rp < count || published < count) {
     bool did = false;
     if (rp < count) {
       const int rs = range_seq % kRedSlots;
-      if (lds_load(&sh.red_count[rs]) == (unsigned)kCompute) {
+      if (written <= range_seq) written = written_min();
+      if (written > range_seq) {
         asm volatile("" ::: "memory");
         f32x4_t a0 = sh.red[rs][0][0][lane], a1 = sh.red[rs][0][1][lane];
 #pragma unroll
@@ -629,8 +749,7 @@ __device__ __forceinline__ void finisher_wave(const ControlCtx& c) {
           a1 += sh.red[rs][w][1][lane];
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        lds_store(&sh.red_count[rs], 0u);
-        lds_store(&sh.red_next[rs], range_seq + kRedSlots);
+        lds_store(&sh.red_freed, range_seq + 1);
         finish_range(c, rp, rb, re, a0, a1);
         ++range_seq;
         r_next_range(re);
@@ -667,15 +786,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(const StackPr
     const StackDesc& d = prog->desc[i];
     sh.seq[i] = SeqDesc{d.w, d.units, (short)d.KT, (short)d.rbw};
   }
-  if (threadIdx.x < kMaxXSlots) {
-    sh.x_ready[threadIdx.x] = 0u;
-    sh.x_done[threadIdx.x] = 0u;
+  if (threadIdx.x < kCompute) {
+    sh.x_used[threadIdx.x] = 0u;
+    sh.red_done[threadIdx.x] = 0u;
   }
-  if (threadIdx.x < kRedSlots) {
-    sh.red_count[threadIdx.x] = 0u;
-    sh.red_next[threadIdx.x] = threadIdx.x;
+  if (threadIdx.x == 0) {
+    sh.x_staged = 0u;
+    sh.red_freed = 0u;
+    sh.error = 0u;
   }
-  if (threadIdx.x == 0) sh.error = 0u;
+  for (int i = threadIdx.x; i < kXRow / 4; i += kThreads) reinterpret_cast<unsigned*>(sh.xzero)[i] = 0u;
   __syncthreads();
 
   if (wave < kCompute) {
