@@ -124,6 +124,9 @@ def main() -> int:
     ap.add_argument("--pmc", action="store_true",
                     help="short run for hardware-counter profiling: a 1 GiB copy of known size, then each "
                          "projection kind once per layer and the lm_head once, no graphs")
+    ap.add_argument("--pmc-prefill", action="store_true",
+                    help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
+                         "M = 2048 and 8192, three launches each, no graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
@@ -181,6 +184,20 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"pmc_run": True, "copy_bytes": 2 * src.numel(),
                           "bytes_per_launch": {n: G.projection_bytes(n, 1) for n in G.projections()}}), flush=True)
+        return 0
+
+    if args.pmc_prefill:
+        p0 = layers[0]
+        weights = {"qkv_proj": p0.qkv, "o_proj": p0.o, "gate_up_proj": p0.gate_up, "down_proj": p0.down}
+        for m in (2048, 8192):
+            for name, pw in weights.items():
+                x = torch.randn((m, pw.k), generator=gen, device=dev).to(torch.bfloat16)
+                epi = _lib.EPI_SILU_MUL if name == "gate_up_proj" else _lib.EPI_NONE
+                for _ in range(3):
+                    kernels.linear(x, pw, epilogue=epi)
+                torch.cuda.synchronize()
+                log(f"prefill {name} M={m}: 3 launches, {G.projection_flops(name, m) / 1e9:.1f} GFLOP each")
+        print(json.dumps({"pmc_prefill_run": True}), flush=True)
         return 0
 
     # --- headline: 36-layer decode step, verify sweep -----------------------
