@@ -180,15 +180,16 @@ typedef struct lsk_projection {
 /* Device bytes of a program of `count` projections. */
 size_t lsk_stack_program_bytes(int count);
 
-/* Device workspace bytes of a program of `count` projections on the current
- * device (it holds per-CU progress words and cross-CU partial sums, so it is
- * sized by the CU count).  The caller zeroes it once before the first
- * launch; every launch leaves its synchronisation words zeroed again (the
- * error word aside, see lsk_stack_error). */
+/* Device workspace bytes of a program of `count` projections (an error word,
+ * the detail record of the first failed wait and one progress word per CU;
+ * 8 KiB).  The caller zeroes it once before the first launch; every launch
+ * leaves its synchronisation words zeroed again (the error word aside, see
+ * lsk_stack_error). */
 size_t lsk_stack_workspace_bytes(int count);
 
-/* Validate `projections` (host array) and upload the program to program_dev
- * (device, lsk_stack_program_bytes(count) bytes).  Synchronous; set-up only. */
+/* Validate `projections` (host array, count = 1..256) and upload the program to
+ * program_dev (device, lsk_stack_program_bytes(count) bytes).  Synchronous;
+ * set-up only. */
 int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void* program_dev,
                       size_t program_bytes);
 

@@ -36,24 +36,18 @@ constexpr unsigned kSkSpinLimit = 1u << 22;
 // Persistent decode-step kernel (stack.hip).
 constexpr int kStackComputeWaves = 8;  // compute waves per workgroup (+1 control wave)
 constexpr int kStackSegTiles = 16;     // k-tiles per K segment of a work pair (K % 512 == 0)
-constexpr int kStackMaxProjections = 512;
+constexpr int kStackMaxProjections = 256;
 constexpr unsigned kStackMagic = 0x4c534b32u;
-// Workspace (32-bit words unless noted): error word, exit counter, one
-// progress word per workgroup, then one partial flag per (projection,
-// workgroup), then one partial slot (kStackPartialBytes) per (projection,
-// workgroup).
+// Workspace (32-bit words): error word, exit counter, the detail record of
+// the first failed wait, and one progress word per workgroup.
 constexpr int kStackWsError = 0;      // nonzero after a bounded wait gave up
 constexpr int kStackWsExit = 1;       // workgroups finished (reset by the last)
 constexpr int kStackWsDetail = 8;     // 8 words: first failed wait (workgroup + 1, code, state)
 constexpr int kStackWsProgress = 64;  // G words: projections completed by each workgroup
-constexpr int kStackMaxGrid = 2048 - kStackWsProgress;
-constexpr size_t kStackPartialBytes = 2048;  // 2 row-blocks x 64 lanes x 16 bytes
-constexpr int kStackWsFlags = 2048;  // count x G words from here
-__host__ __device__ constexpr size_t kStackWsPartialsOffset(int count, int G) {
-  return (((size_t)kStackWsFlags + (size_t)count * G) * 4 + 255) / 256 * 256;
-}
+constexpr int kStackWsWords = 2048;
+constexpr int kStackMaxGrid = kStackWsWords - kStackWsProgress;
 __host__ __device__ constexpr size_t kStackWsBytes(int count, int G) {
-  return kStackWsPartialsOffset(count, G) + (size_t)count * G * kStackPartialBytes;
+  return (void)count, (void)G, (size_t)kStackWsWords * 4;
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

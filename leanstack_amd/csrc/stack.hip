@@ -11,44 +11,39 @@
 //
 // Work split.  A projection of U units (16 weight rows, or a 32-row gate/up
 // pair for SiLU*up) and K = NS segments of 512 is a list of U*NS
-// (unit, segment) pairs, unit-major; workgroup g takes pairs
-// [g*P/G, (g+1)*P/G).  Every CU so streams the same number of bytes of every
-// projection (within one pair), whatever U is -- 160 units of o_proj and
-// down_proj against 256 CUs included.
+// (unit, segment) pairs, unit-major; workgroup g takes the whole units
+// [g*U/G, (g+1)*U/G), so every unit's sum stays inside one workgroup.  When
+// U < G (o_proj and down_proj: 160 units), the workgroups without a unit go
+// straight on to the next projection's weights.
 //
-// Roles inside the workgroup (9 waves):
+// Roles inside the workgroup (10 waves):
 //  * 8 compute waves.  Wave w takes k-tiles 2w, 2w+1 of every segment, for
-//    every row-block of the pair, so each wave's stream of 1 KB weight tiles
+//    every row-block of the unit, so each wave's stream of 1 KB weight tiles
 //    is fixed by the program.  A wave keeps kRing tile loads in flight in
 //    registers and refills a slot as soon as it is multiplied, so the only
 //    memory waits it has are for its own oldest weight load.  Activation
-//    fragments come from LDS (staged by the control wave); accumulators of a
-//    finished unit range go to LDS for the control wave.
-//  * 1 control wave.  It stages each pair's activation segment into a ring
-//    of LDS slots (coherent loads, after the projection's dependency is
-//    met), sums the 8 compute waves' partials of each unit range in wave
-//    order, and finishes units: a unit wholly inside the workgroup's range
-//    is stored with its epilogue; a unit that later workgroups finish is
-//    "owned" here (this workgroup has its segment 0): the owner waits for
-//    their fp32 partials, adds them in workgroup order and stores; a unit
-//    this workgroup enters mid-K is published as a partial for its owner.
-//    After its last unit range of a projection it publishes its progress
-//    word (projections completed).  A projection that depends on q starts
-//    staging activations once every workgroup's progress exceeds q.  The
-//    control wave never blocks on one of these while other work is ready,
-//    so a workgroup always finishes what other workgroups wait for.
+//    fragments come from LDS (staged by the stager); the accumulators of a
+//    finished unit go to LDS for the finisher.
+//  * The stager stages each pair's activation segment into a ring of LDS
+//    slots (device-coherent loads when the input is produced inside the
+//    launch), once every workgroup's progress shows the projection's
+//    dependency complete.
+//  * The finisher sums the 8 compute waves' accumulators of each unit in
+//    wave order, stores the unit with its epilogue and, after a projection's
+//    last unit, publishes this workgroup's progress word (projections
+//    completed).
+// Neither control wave blocks on a wait while work that others wait for is
+// ready, so a workgroup always finishes what other workgroups wait for.
 //
-// Every sum has a fixed order (waves, then workgroups), so results are
-// bitwise reproducible.  Activations, residuals, outputs, partials and
-// progress cross XCDs, whose L2s are not coherent with each other, so they
-// are read and written with agent-scope relaxed atomics (device-coherent
-// loads and stores; no cache maintenance).  Owners wait only for later
-// workgroups' partials and dependencies point to earlier projections, so
-// the waits always drain with the whole grid resident (one workgroup per
-// CU); every wait is bounded anyway and records an error instead of
-// spinning forever.  The last workgroup out clears the progress words, and
-// owners clear the partial flags they consumed, so the workspace is
-// reusable by the next launch (and by graph replays) without a memset.
+// Every sum has a fixed order, so results are bitwise reproducible.
+// Activations, residuals, outputs and progress cross XCDs, whose L2s are not
+// coherent with each other, so they are read and written with agent-scope
+// relaxed atomics (device-coherent loads and stores; no cache maintenance).
+// Dependencies point to earlier projections and the whole grid is resident
+// (one workgroup per CU), so the waits always drain; every wait is bounded
+// anyway and records an error instead of spinning forever.  The last
+// workgroup out clears the progress words, so the workspace is reusable by
+// the next launch (and by graph replays) without a memset.
 
 #include <hip/hip_runtime.h>
 
@@ -64,12 +59,15 @@ constexpr int kCompute = kStackComputeWaves;          // 8
 constexpr int kThreads = (kCompute + 2) * 64;         // + stager and finisher waves
 constexpr int kSeg = kStackSegTiles;                  // 16 k-tiles (512 K) per segment
 constexpr int kWaveTiles = kSeg / kCompute;           // 2 k-tiles per compute wave per segment
-constexpr int kRing = 16;                             // weight tiles in flight per compute wave
+#ifndef LSK_RING
+#define LSK_RING 16
+#endif
+constexpr int kRing = LSK_RING;                             // weight tiles in flight per compute wave
 constexpr int kXRow = kSeg * kTileK * 2 + 16;         // LDS bytes per activation row (+16: bank skew)
-constexpr int kXBytes = 116 * 1024;                   // staged activation segments (M rows each)
-constexpr int kMaxXSlots = 16;
+constexpr int kXBytes = 104 * 1024;                   // staged activation segments (M rows each)
+constexpr int kMaxXSlots = 64;
 constexpr int kRedSlots = 2;
-constexpr unsigned kSpinLimit = 1u << 22;   // polls of one LDS or partial-flag wait
+constexpr unsigned kSpinLimit = 1u << 22;   // polls of one LDS wait
 constexpr unsigned kIdleLimit = 1u << 20;   // control-wave rounds without progress
 
 
@@ -179,6 +177,7 @@ struct SeqDesc {
 };
 
 struct Shared {
+  StackDesc desc[kStackMaxProjections];                // the program, for the stager and finisher
   SeqDesc seq[kStackMaxProjections];
   unsigned char xbuf[kXBytes];                         // staged activation segments
   unsigned char xzero[kXRow];                          // zeros: the fragment of tokens >= M
@@ -190,9 +189,26 @@ struct Shared {
   unsigned error;                                      // a bounded wait inside the workgroup gave up
 };
 
-// Pairs [begin, end) of workgroup g in a projection of P pairs.
-// (P * G < 2^32: packed weights are under 4 GiB and G <= kStackMaxGrid.)
-__device__ __forceinline__ int range_begin(int P, int G, int g) { return (int)((unsigned)P * (unsigned)g / (unsigned)G); }
+// Projection p's descriptor from the LDS copy, every word made wave-uniform
+// (control waves branch and address on it; a scalar-cache miss on the
+// program in global memory costs a memory round trip under the weight stream).
+__device__ __forceinline__ StackDesc lds_desc(const Shared& sh, int p) {
+  static_assert(sizeof(StackDesc) % 4 == 0, "descriptor copied as 32-bit words");
+  constexpr int kWords = sizeof(StackDesc) / 4;
+  unsigned w[kWords];
+  const unsigned* src = reinterpret_cast<const unsigned*>(&sh.desc[p]);
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) w[i] = uni(src[i]);
+  return __builtin_bit_cast(StackDesc, w);
+}
+
+// First pair of workgroup g in a projection of `units` units of NS pairs:
+// workgroup g takes whole units [units*g/G, units*(g+1)/G), so no unit's sum
+// is split between workgroups (units * G < 2^32: packed weights are under
+// 4 GiB and G <= kStackMaxGrid).
+__device__ __forceinline__ int range_begin(int units, int NS, int G, int g) {
+  return (int)((unsigned)units * (unsigned)g / (unsigned)G) * NS;
+}
 
 // Raw buffer resource over `bytes` bytes at `base` (wave-uniform).
 constexpr int kNonTemporal = 2;  // buffer-load cache policy: streamed once
@@ -221,9 +237,9 @@ struct Share {
     KT = uni((int)d.KT);
     NS = KT / kSeg;
     R = uni((int)d.rbw);
-    const unsigned P = (unsigned)uni(d.units) * (unsigned)NS;
-    b = (int)(P * (unsigned)g / (unsigned)G);
-    e = (int)(P * (unsigned)(g + 1) / (unsigned)G);
+    const int units = uni(d.units);
+    b = range_begin(units, NS, G, g);
+    e = range_begin(units, NS, G, g + 1);
   }
 };
 
@@ -446,8 +462,6 @@ struct ControlCtx {
   Shared* sh;
   unsigned* ws;
   unsigned* progress;   // G words
-  unsigned* flags;      // count x G words
-  unsigned char* parts; // count x G partial slots of kStackPartialBytes
   int G, g, lane, M;
 };
 
@@ -508,63 +522,10 @@ __device__ __forceinline__ void store_unit(const ControlCtx& c, const StackDesc&
   coherent_store64(d.y + (size_t)m * d.ldy + n, packed);
 }
 
-__device__ __forceinline__ unsigned char* partial_slot(const ControlCtx& c, int p, int g) {
-  return c.parts + ((size_t)p * c.G + g) * kStackPartialBytes;
-}
-
-__device__ __forceinline__ void store_partial(unsigned char* slot, int lane, const f32x4_t& v) {
-  unsigned long long* q = reinterpret_cast<unsigned long long*>(slot + lane * 16);
-  coherent_store64(q, (unsigned long long)__float_as_uint(v[0]) | ((unsigned long long)__float_as_uint(v[1]) << 32));
-  coherent_store64(q + 1, (unsigned long long)__float_as_uint(v[2]) | ((unsigned long long)__float_as_uint(v[3]) << 32));
-}
-
-__device__ __forceinline__ void add_partial(f32x4_t& v, const unsigned char* slot, int lane) {
-  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(slot + lane * 16);
-  const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
-  v[0] += __uint_as_float((unsigned)lo);
-  v[1] += __uint_as_float((unsigned)(lo >> 32));
-  v[2] += __uint_as_float((unsigned)hi);
-  v[3] += __uint_as_float((unsigned)(hi >> 32));
-}
-
-// Finish the unit range [pb, pe) of projection p (summed accumulators a0, a1).
-__device__ void finish_range(const ControlCtx& c, int p, int pb, int pe, f32x4_t a0, f32x4_t a1) {
-  const StackDesc& d = c.prog->desc[p];
-  const int NS = d.KT / kSeg;
-  const int P = d.units * NS;
-  const int unit = pb / NS;
-  const int unit_end = (unit + 1) * NS;
-  if (pb % NS != 0) {
-    // Entered mid-K: publish the partial for the owner (an earlier workgroup).
-    unsigned char* slot = partial_slot(c, p, c.g);
-    store_partial(slot, c.lane, a0);
-    if (d.rbw == 2) store_partial(slot + 1024, c.lane, a1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (c.lane == 0) coherent_store32(c.flags + (size_t)p * c.G + c.g, 1u);
-    return;
-  }
-  // Owner: add the partials of the later workgroups that finish the unit.
-  for (int j = c.g + 1, covered = pe; covered < unit_end && j < c.G; ++j) {
-    const int jb = range_begin(P, c.G, j), je = range_begin(P, c.G, j + 1);
-    if (je > jb) {
-      unsigned* flag = c.flags + (size_t)p * c.G + j;
-      unsigned spins = 0;
-      while (coherent_load32(flag) == 0u && coherent_load32(c.ws + kStackWsError) == 0u) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins > kSpinLimit) {
-          record_error(c, 4u, (unsigned)p, (unsigned)j, (unsigned)pb, (unsigned)pe);
-          break;
-        }
-      }
-      asm volatile("" ::: "memory");
-      const unsigned char* slot = partial_slot(c, p, j);
-      add_partial(a0, slot, c.lane);
-      if (d.rbw == 2) add_partial(a1, slot + 1024, c.lane);
-      if (c.lane == 0) coherent_store32(flag, 0u);
-    }
-    covered = je;
-  }
-  store_unit(c, d, unit, a0, a1);
+// The summed accumulators of unit `unit` of projection p (every unit range
+// is a whole unit: workgroups take whole units).
+__device__ __forceinline__ void finish_unit(const ControlCtx& c, int p, int unit, f32x4_t a0, f32x4_t a1) {
+  store_unit(c, lds_desc(*c.sh, p), unit, a0, a1);
 }
 
 // A bounded wait of a control wave has gone on too long, or another wave or
@@ -580,43 +541,44 @@ __device__ __forceinline__ bool give_up(const ControlCtx& c, unsigned& idle, uns
 }
 
 // Stager: activation segments of this workgroup's pairs, in pair order, into
-// the LDS slots.  A batch takes the next pairs whose slot is free and whose
-// dependency is met, up to kBatchRows activation rows (M per pair); all its
-// row loads are issued before the first is written to LDS, so a batch costs
-// one memory round trip.  (Plain coherent loads and LDS stores: an LDS DMA
-// anywhere in the kernel makes the compiler wait for all vector memory
-// before every LDS read, which would drain the compute waves' weight rings.)
+// the LDS slots.  A batch is the next run of one projection's pairs whose
+// slots are free (once the projection's dependency is met), up to kBatchRows
+// activation rows (M per pair); all its row loads are issued before the
+// first is written to LDS, so a batch costs one memory round trip, and the
+// projection's descriptor stays in registers for the whole run.  (Plain
+// loads and LDS stores: an LDS DMA anywhere in the kernel makes the compiler
+// wait for all vector memory before every LDS read, which would drain the
+// compute waves' weight rings.)
 constexpr int kBatchRows = 16;
-
-struct XCursor {
-  int xp, xpair, xend, xbegin;
-  unsigned seq;
-};
 
 __device__ __forceinline__ void stager_wave(const ControlCtx& c) {
   const StackProgram* prog = c.prog;
   Shared& sh = *c.sh;
   const int G = c.G, g = c.g, count = prog->count, M = c.M, lane = c.lane;
-  auto enter = [&](XCursor& x, int from) {
-    for (x.xp = from; x.xp < count; ++x.xp) {
-      const StackDesc& d = prog->desc[x.xp];
-      const int P = d.units * (d.KT / kSeg);
-      x.xpair = range_begin(P, G, g);
-      x.xend = range_begin(P, G, g + 1);
-      x.xbegin = x.xpair;
-      if (x.xpair < x.xend) return;
+  const int nslots = x_slots(M);
+  const unsigned slot_bytes = (unsigned)(M * kXRow);
+  const int batch_pairs = kBatchRows / M;  // >= 1: M <= 16
+
+  // Projection xp being staged: its pairs [xpair, xend), activation rows.
+  int xp = 0, xpair = 0, xend = 0, xbegin = 0, NS = 1, ldx = 0, dep = -1;
+  const __bf16* xbase = nullptr;
+  auto enter = [&](int from) {
+    for (xp = from; xp < count; ++xp) {
+      const StackDesc d = lds_desc(sh, xp);
+      NS = d.KT / kSeg;
+      xpair = range_begin(d.units, NS, G, g);
+      xend = range_begin(d.units, NS, G, g + 1);
+      if (xpair < xend) {
+        xbegin = xpair;
+        xbase = d.x;
+        ldx = d.ldx;
+        dep = d.dep;
+        return;
+      }
     }
   };
-  auto next_pair = [&](XCursor& x) {
-    ++x.seq;
-    if (++x.xpair >= x.xend) enter(x, x.xp + 1);
-  };
-  XCursor cur{0, 0, 0, 0, 0u};
-  enter(cur, 0);
-  unsigned idle = 0;
-  int dep_ok = -1;  // projections <= dep_ok are known complete everywhere
-  const int nslots = x_slots(M);
-  const int slot_bytes = M * kXRow;
+  enter(0);
+
   // Pairs every compute wave has read.
   auto used_min = [&]() {
     unsigned v[kCompute];
@@ -627,91 +589,108 @@ __device__ __forceinline__ void stager_wave(const ControlCtx& c) {
     for (int w = 1; w < kCompute; ++w) m = v[w] < m ? v[w] : m;
     return uni(m);
   };
-  unsigned used = 0;
+  unsigned seq = 0, used = 0, idle = 0;
+  int dep_ok = -1;  // projections <= dep_ok are known complete everywhere
+  int slot = 0;     // seq % nslots
 
-  // Row r of the batch that starts at cursor b: f(r, source, LDS destination).
-  auto walk = [&](const XCursor& b, int nrows, auto&& f) {
-    XCursor x = b;
-    int m = 0;
-    unroll<kBatchRows>([&](auto rc) {
-      constexpr int r = decltype(rc)::value;
-      if (r < nrows) {
-        const StackDesc& d = prog->desc[x.xp];
-        const int seg = x.xpair % (d.KT / kSeg);
-        f(IntC<r>{}, d.x + (size_t)m * d.ldx + (size_t)seg * kSeg * kTileK + 8 * lane,
-          sh.xbuf + (x.seq % nslots) * slot_bytes + m * kXRow + 16 * lane, d.dep >= 0);
-        if (++m == M) {
-          m = 0;
-          next_pair(x);
-        }
+  while (xp < count) {
+    if (dep > dep_ok) {
+      if (!projections_done(c, dep)) {
+        __builtin_amdgcn_s_sleep(1);
+        if (give_up(c, idle, 5u, (unsigned)xp, seq)) return;
+        continue;
       }
-    });
-  };
-
-  while (cur.xp < count) {
-    // Collect the batch.
-    const XCursor start = cur;
-    int nrows = 0;
-    while (cur.xp < count && nrows + M <= kBatchRows) {
-      if (cur.seq >= used + (unsigned)nslots) {  // the slot's previous pair may still be read
-        used = used_min();
-        if (cur.seq >= used + (unsigned)nslots) break;
-      }
-      const StackDesc& d = prog->desc[cur.xp];
-      if (d.dep > dep_ok) {
-        if (!projections_done(c, d.dep)) break;
-        dep_ok = d.dep;
-        LSK_TRACE(c.ws, count, G, g, cur.xp, 0, lane);
-      }
-      nrows += M;
-      next_pair(cur);
+      dep_ok = dep;
+      LSK_TRACE(c.ws, count, G, g, xp, 0, lane);
     }
-    if (nrows == 0) {
+    // Slot of pair seq + i is free once every wave has read pair seq + i - nslots.
+    if (seq >= used + (unsigned)nslots) used = used_min();
+    const int free_slots = (int)(used + (unsigned)nslots - seq);
+    if (free_slots <= 0) {
       __builtin_amdgcn_s_sleep(1);
-      if (give_up(c, idle, 5u, (unsigned)cur.xp, cur.seq)) return;
+      if (give_up(c, idle, 5u, (unsigned)xp, seq)) return;
       continue;
     }
     idle = 0;
+    int n = xend - xpair;
+    n = n < free_slots ? n : free_slots;
+    n = n < batch_pairs ? n : batch_pairs;
+    const int nrows = n * M;
+    if (xpair == xbegin) LSK_TRACE(c.ws, count, G, g, xp, 6, lane);
+
+    // Row r of the batch: pair xpair + r / M, activation row r % M.
     u32x4_t rows[kBatchRows];
-    // Inputs ready at launch (no dependency) are not written by the program,
-    // so plain cacheable loads see them (and the XCD's L2 serves the other
-    // workgroups); inputs the program produces need device-coherent loads.
-    walk(start, nrows, [&](auto rc, const __bf16* src, unsigned char*, bool coherent) {
-      if (coherent) {
-        const unsigned long long* q = reinterpret_cast<const unsigned long long*>(src);
-        const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
-        rows[decltype(rc)::value] = u32x4_t{(unsigned)lo, (unsigned)(lo >> 32), (unsigned)hi, (unsigned)(hi >> 32)};
-      } else {
-        rows[decltype(rc)::value] = *reinterpret_cast<const u32x4_t*>(src);
-      }
-    });
-    walk(start, nrows, [&](auto rc, const __bf16*, unsigned char* dst, bool) {
-      *reinterpret_cast<u32x4_t*>(dst) = rows[decltype(rc)::value];
-    });
+    {
+      int m = 0, seg = xpair % NS;
+      const __bf16* src = xbase + (size_t)seg * kSeg * kTileK + 8 * lane;
+      unroll<kBatchRows>([&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        if (r < nrows) {
+          const __bf16* row = src + (size_t)m * ldx;
+          if (dep >= 0) {
+            // Produced inside this launch by other workgroups: device-coherent loads.
+            const unsigned long long* q = reinterpret_cast<const unsigned long long*>(row);
+            const unsigned long long lo = coherent_load64(q), hi = coherent_load64(q + 1);
+            rows[r] = u32x4_t{(unsigned)lo, (unsigned)(lo >> 32), (unsigned)hi, (unsigned)(hi >> 32)};
+          } else {
+            // Ready at launch and never written by the program: plain cached loads.
+            rows[r] = *reinterpret_cast<const u32x4_t*>(row);
+          }
+          if (++m == M) {
+            m = 0;
+            if (++seg == NS) seg = 0;
+            src = xbase + (size_t)seg * kSeg * kTileK + 8 * lane;
+          }
+        }
+      });
+    }
+#ifdef LSK_STACK_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (xpair == xbegin) LSK_TRACE(c.ws, count, G, g, xp, 7, lane);
+#endif
+    {
+      int m = 0, sl = slot;
+      unsigned char* dst = sh.xbuf + (unsigned)sl * slot_bytes + 16 * lane;
+      unroll<kBatchRows>([&](auto rc) {
+        constexpr int r = decltype(rc)::value;
+        if (r < nrows) {
+          *reinterpret_cast<u32x4_t*>(dst + m * kXRow) = rows[r];
+          if (++m == M) {
+            m = 0;
+            if (++sl == nslots) sl = 0;
+            dst = sh.xbuf + (unsigned)sl * slot_bytes + 16 * lane;
+          }
+        }
+      });
+    }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    lds_store(&sh.x_staged, cur.seq);
-    if (start.xpair == start.xbegin) LSK_TRACE(c.ws, count, G, g, start.xp, 1, lane);
+    seq += (unsigned)n;
+    lds_store(&sh.x_staged, seq);
+    if (xpair == xbegin) LSK_TRACE(c.ws, count, G, g, xp, 1, lane);
+    slot = (slot + n) % nslots;
+    xpair += n;
+    if (xpair == xend) enter(xp + 1);
   }
 }
 
-// Finisher: the compute waves' partials of each unit range, in order, then
-// the range's epilogue or cross-workgroup partial, and this workgroup's
-// progress word after its last range of each projection.
+// Finisher: the compute waves' accumulators of each unit, in order, then
+// the unit's epilogue and store, and this workgroup's progress word after
+// its last unit of each projection.
 __device__ __forceinline__ void finisher_wave(const ControlCtx& c) {
   const StackProgram* prog = c.prog;
   Shared& sh = *c.sh;
   const int G = c.G, g = c.g, count = prog->count, lane = c.lane;
-  int rp = 0, rb = 0, re = 0, rend = 0;
+  int rp = 0, rb = 0, re = 0, rend = 0, rns = 1;
   auto r_next_range = [&](int from_pair) {
     // First unit range starting at pair from_pair of projection rp, or the next projection's first.
     while (rp < count) {
-      const StackDesc& d = prog->desc[rp];
+      const StackDesc d = lds_desc(sh, rp);
       const int NS = d.KT / kSeg;
-      const int P = d.units * NS;
-      if (from_pair < 0) from_pair = range_begin(P, G, g);
-      rend = range_begin(P, G, g + 1);
+      if (from_pair < 0) from_pair = range_begin(d.units, NS, G, g);
+      rend = range_begin(d.units, NS, G, g + 1);
       if (from_pair < rend) {
         rb = from_pair;
+        rns = NS;
         const int unit_end = (from_pair / NS + 1) * NS;
         re = unit_end < rend ? unit_end : rend;
         return;
@@ -750,7 +729,7 @@ __device__ __forceinline__ void finisher_wave(const ControlCtx& c) {
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         lds_store(&sh.red_freed, range_seq + 1);
-        finish_range(c, rp, rb, re, a0, a1);
+        finish_unit(c, rp, rb / rns, a0, a1);
         ++range_seq;
         r_next_range(re);
         did = true;
@@ -758,7 +737,7 @@ __device__ __forceinline__ void finisher_wave(const ControlCtx& c) {
     }
     if (published < rp) {
       LSK_TRACE(c.ws, count, G, g, rp - 1, 4, lane);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // outputs and partials stored
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // outputs stored
       published = rp;
       if (lane == 0) coherent_store32(c.progress + g, (unsigned)published);
       LSK_TRACE(c.ws, count, G, g, rp - 1, 5, lane);
@@ -786,6 +765,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(const StackPr
     const StackDesc& d = prog->desc[i];
     sh.seq[i] = SeqDesc{d.w, d.units, (short)d.KT, (short)d.rbw};
   }
+  {
+    constexpr int kWords = sizeof(StackDesc) / 4;
+    const unsigned* src = reinterpret_cast<const unsigned*>(prog->desc);
+    unsigned* dst = reinterpret_cast<unsigned*>(sh.desc);
+    for (int i = threadIdx.x; i < prog->count * kWords; i += kThreads) dst[i] = src[i];
+  }
   if (threadIdx.x < kCompute) {
     sh.x_used[threadIdx.x] = 0u;
     sh.red_done[threadIdx.x] = 0u;
@@ -801,9 +786,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(const StackPr
   if (wave < kCompute) {
     compute_wave(prog, sh, ws, wave, lane);
   } else {
-    ControlCtx c{prog, &sh, ws, ws + kStackWsProgress, ws + kStackWsFlags, nullptr, (int)gridDim.x,
-                 (int)blockIdx.x, lane, prog->M};
-    c.parts = reinterpret_cast<unsigned char*>(ws) + kStackWsPartialsOffset(prog->count, (int)gridDim.x);
+    ControlCtx c{prog, &sh, ws, ws + kStackWsProgress, (int)gridDim.x, (int)blockIdx.x, lane, prog->M};
     if (wave == kCompute)
       stager_wave(c);
     else
