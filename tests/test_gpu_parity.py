@@ -253,3 +253,38 @@ def test_split_k_workspace_contract(gpu):
     assert kernels.linear_error(ws) == 0
     with pytest.raises(ValueError):
         kernels.linear(x.to(dev), pw, workspace=ws[: nbytes // 2])
+
+
+def _prefill_case(name, m, seed):
+    if name == "gate_up_proj":
+        n, k = 2 * G.intermediate_size, G.hidden_size
+        return weight(n, k, seed=seed), activations(m, k, seed=seed + 1), _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL
+    n, k = PROJ[name]
+    return weight(n, k, seed=seed), activations(m, k, seed=seed + 1), _lib.LAYOUT_MFMA16X32, _lib.EPI_NONE
+
+
+def _oracle(x, w, epilogue):
+    y = ref.linear(x, w)
+    return ref.silu_mul(y, G.intermediate_size) if epilogue == _lib.EPI_SILU_MUL else y
+
+
+@pytest.mark.parametrize("name", sorted(PROJ) + ["gate_up_proj"])
+def test_prefill_m512_full_shapes(gpu, name):
+    """M=512 (the smallest prefill bucket of the benchmark) at every projection shape."""
+    w, x, layout, epi = _prefill_case(name, 512, seed=91)
+    y = _gpu_linear(x, w, layout, epi)
+    assert_parity(y, _oracle(x, w, epi), f"{name} prefill M=512")
+
+
+@pytest.mark.parametrize("name", sorted(PROJ) + ["gate_up_proj"])
+def test_prefill_m8192_sampled_rows(gpu, name):
+    """M=8192 at every projection shape: the whole GEMM runs on the GPU; output
+    rows depend only on their own activation row, so the oracle checks a
+    sample of rows (block edges, the last row, and random rows)."""
+    m = 8192
+    w, x, layout, epi = _prefill_case(name, m, seed=93)
+    y = _gpu_linear(x, w, layout, epi)
+    gen = torch.Generator().manual_seed(94)
+    rows = torch.cat([torch.tensor([0, 1, 255, 256, 4095, 4096, 8190, 8191]),
+                      torch.randint(0, m, (56,), generator=gen)]).unique()
+    assert_parity(y[rows], _oracle(x[rows], w, epi), f"{name} prefill M=8192 (rows sampled)")
