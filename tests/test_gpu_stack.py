@@ -74,7 +74,7 @@ def _oracle_chain(ws_rows, x0_cpu, layers):
     return outs
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 4, 8, 16])
 def test_stack_dependency_chain_matches_oracle(gpu, m):
     layers = 2
     ws_rows = [_layer_weights(100 * l + 7) for l in range(layers)]
