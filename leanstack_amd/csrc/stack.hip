@@ -122,6 +122,9 @@ __device__ __forceinline__ void coherent_store32(unsigned* p, unsigned v) {
 // Optional event timestamps (build with -DLSK_STACK_TRACE): word
 // (g * count + p) * 8 + event of a buffer placed right after the workspace
 // receives the constant-clock time of the event for workgroup g, projection p.
+// Events: 0 dependency seen met, 6 first batch sized, 7 its loads landed,
+// 1 first activations staged, 2 first multiply, 3 last multiply, 4 last unit
+// stored, 5 progress published.
 #ifdef LSK_STACK_TRACE
 #define LSK_TRACE(ws_, count_, G_, g_, p_, ev_, lane_)                                                             \
   do {                                                                                                            \
@@ -130,8 +133,8 @@ __device__ __forceinline__ void coherent_store32(unsigned* p, unsigned v) {
                                        ((size_t)(g_) * (count_) + (p_)) * 8 + (ev_)),                             \
                          (unsigned)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); \
   } while (0)
-// Per compute wave: cycles in the ring wait, the activation wait, the
-// partial-slot wait, and in total, at word (G*count*8) + (g*8 + wave)*4 + i.
+// Per compute wave: 0, cycles in the activation wait, in the accumulator-slot
+// wait, and in total, at word (G*count*8) + (g*8 + wave)*4 + i.
 #define LSK_STALL_BEGIN() const unsigned long long stall_t0_ = __builtin_amdgcn_s_memtime()
 #define LSK_STALL_END(acc_) (acc_) += __builtin_amdgcn_s_memtime() - stall_t0_
 #else
