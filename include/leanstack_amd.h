@@ -115,9 +115,10 @@ int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* 
  *              runs the prefill MFMA GEMM.
  *   workspace  NULL, or (prefill) lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K)
  *              bytes, 256-byte aligned, zero-filled before its first use.
- *              With it, the prefill GEMM splits the K range of its output
- *              blocks over all CUs (stream-K) and adds the fp32 partials in a
- *              fixed order; without it, one workgroup per output block.  Calls
+ *              With it, the prefill GEMM splits the K range of the output
+ *              blocks of its last, partial round over the idle CUs (split-K)
+ *              and adds the fp32 partials in a fixed order; without it, one
+ *              workgroup per output block.  Calls
  *              leave it as they found it (see lsk_linear_error); calls that
  *              share one must be stream-ordered.  Ignored for M <= 16.
  * Replaces torch.mv / F.linear at src/leanstack/runtime/qwen_explicit.py:748,
@@ -205,7 +206,7 @@ int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws
 int lsk_stack_error(void* workspace, int* error_out);
 
 /* Read (synchronously) and clear the error word of a prefill workspace:
- * 0 = every wait of every stream-K launch since the last call completed;
+ * 0 = every wait of every split-K launch since the last call completed;
  * nonzero = a bounded wait for another workgroup's partial gave up (outputs
  * of that launch are invalid).  No counterpart in the reference, whose
  * library GEMMs have no cross-workgroup waits. */

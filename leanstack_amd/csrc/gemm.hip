@@ -945,9 +945,9 @@ namespace {
 
 bool sk_shape(int M, int N, int K) { return M > kGemmBM && N % wdx::BN == 0 && K % (2 * wdx::BK) == 0; }
 
-// Persistent stream-K grid on `device`: every CU's resident workgroups
-// (the kernel holds 512 registers per lane, so one per CU), capped by the
-// workspace's flag capacity.  Cached per device.
+// Workgroups resident at once on `device` (the kernel holds 512 registers
+// per lane, so one per CU), capped by the workspace's flag capacity: the
+// split-K plan spreads the last round over this many.  Cached per device.
 hipError_t sk_grid(int device, int* grid_out) {
   static std::mutex mu;
   static std::vector<int> cache;

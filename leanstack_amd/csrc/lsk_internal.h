@@ -22,11 +22,11 @@ constexpr int kGemmBN = 128;
 constexpr int kGemmBM = 128;
 constexpr int kGemmBK = 64;
 
-// Stream-K prefill workspace (gemm.hip): word 0 is the error word (nonzero
-// after a bounded wait gave up), one flag word per workgroup from
-// kSkFlagsOffset, one fp32 256x256 partial block per workgroup from
-// kSkPartialsOffset.  Zero-filled before first use; every launch leaves the
-// flags zero.
+// Split-K prefill workspace (gemm.hip): word 0 is the error word (nonzero
+// after a bounded wait gave up), an arrival and a departure word per split
+// output block from kSkFlagsOffset, one fp32 256x256 partial block per split
+// workgroup from kSkPartialsOffset.  Zero-filled before first use; every
+// launch leaves the flags zero.
 constexpr size_t kSkFlagsOffset = 256;
 constexpr size_t kSkPartialsOffset = 8192;
 constexpr size_t kSkPartialBytes = 256 * 256 * 4;
@@ -100,13 +100,14 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
                                  float* logits, int logits_bf16, long long* out_idx,
                                  ArgmaxPartial* partials, hipStream_t stream);
 
-// Workspace bytes the stream-K prefill path needs on `device` for this shape
+// Workspace bytes the split-K prefill path needs on `device` for this shape
 // (0 when the shape does not take it).  Sets *status to a HIP error if the
 // device query fails.
 size_t gemm_workspace_bytes(int device, int M, int N, int K, hipError_t* status);
 
 // Prefill GEMM launch (any M >= 1; used for M > kDecodeMaxM).  With a
-// workspace of at least gemm_workspace_bytes() the stream-K kernel runs;
+// workspace of at least gemm_workspace_bytes() the last partial round of
+// output blocks is split along K over the idle CUs;
 // with none, one workgroup per output block.
 hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M, int ldx,
                               void* y, int ldy, Epilogue epi, const void* residual, int ldr,

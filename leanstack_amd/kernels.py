@@ -43,7 +43,7 @@ _prefill_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def prefill_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor | None:
-    """The stream-K workspace of the prefill GEMM for the current stream of
+    """The split-K workspace of the prefill GEMM for the current stream of
     `device` (zero-filled once, left zero-filled by every call), or None when
     the shape does not use one.  One per (device, stream), because calls that
     share a workspace must be stream-ordered."""
@@ -73,7 +73,7 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
 
     epilogue EPI_NONE (N' = N), EPI_SILU_MUL (gate_up layout, N' = N/2,
     SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection).
-    workspace: "auto" uses the per-stream stream-K workspace for prefill
+    workspace: "auto" uses the per-stream split-K workspace for prefill
     shapes (prefill_workspace), None runs one workgroup per output block, a
     uint8 device tensor is used as given."""
     if not isinstance(weight, PackedWeight):
