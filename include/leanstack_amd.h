@@ -129,6 +129,25 @@ int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K,
                     int epilogue, const void* residual, int ldr,
                     void* workspace, size_t ws_bytes, void* hip_stream);
 
+/* y[M][*] = epilogue(rms_norm(x)[M][K] . W[N][K]^T) for M = 1..16, with
+ *   rms_norm(x)[m][k] = bf16((x[m][k] * r[m]) * norm_weight[k]),
+ *   r[m] = 1 / sqrt(sum_k x[m][k]^2 / K + eps), fp32 arithmetic,
+ * the RMSNorm computed inside the projection kernel (no normalised copy of x
+ * is written).  Arguments as for lsk_linear_bf16 (workspace: none), plus
+ *   norm_weight  device bf16 [K], 16-byte aligned
+ *   eps          finite, >= 0
+ * Replaces the F.rms_norm in front of the decode / verify QKV and gate_up
+ * projections: qwen_rmsnorm_vector + torch.mv at
+ * src/leanstack/runtime/qwen_explicit.py:1255 (input_layernorm, then QKV at
+ * :787) and :941-942 (post_attention_layernorm, then gate_up), and
+ * F.rms_norm + F.linear at :821-827 for the verify rows. */
+int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K,
+                            const void* x, int M, int ldx,
+                            const void* norm_weight, float eps,
+                            void* y, int ldy,
+                            int epilogue, const void* residual, int ldr,
+                            void* hip_stream);
+
 /* Greedy lm_head: out_idx[m] = argmax_v sum_k f32(W[v][k]) * f32(x[m][k]) for
  * m < M (M = 1..16), lowest index on ties.
  *   logits_mode  LSK_LOGITS_FP32 compares fp32 scores, as the cuTile kernel

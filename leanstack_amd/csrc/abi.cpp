@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -74,6 +75,31 @@ inline size_t packed_unit(int K, int pr, int k8) {
   const int kt = k8 / 4;
   const int gq = k8 % 4;
   return ((size_t)rb * KT + kt) * 64 + (size_t)gq * 16 + r;
+}
+
+// Argument rules shared by the projection entry points (see lsk_linear_bf16).
+int check_linear_args(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx,
+                      const void* y, int ldy, int epilogue, const void* residual, int ldr) {
+  if (int st = check_shape(layout_id, N, K)) return st;
+  if (epilogue != LSK_EPI_NONE && epilogue != LSK_EPI_SILU_MUL && epilogue != LSK_EPI_RESIDUAL_ADD)
+    return fail(LSK_ERR_INVALID, "unknown epilogue %d", epilogue);
+  if ((epilogue == LSK_EPI_SILU_MUL) != (layout_id == LSK_LAYOUT_MFMA16X32_GATEUP))
+    return fail(LSK_ERR_INVALID, "the SiLU*up epilogue requires the interleaved gate_up layout and vice versa");
+  if (M < 1) return fail(LSK_ERR_INVALID, "M=%d must be >= 1", M);
+  if (w_packed == nullptr || x == nullptr || y == nullptr) return fail(LSK_ERR_INVALID, "null device pointer");
+  if (!aligned(w_packed, 16)) return fail(LSK_ERR_INVALID, "packed weights must be 16-byte aligned");
+  if (ldx < K || ldx % 8 != 0 || !aligned(x, 16))
+    return fail(LSK_ERR_INVALID, "x needs ldx >= K, ldx %% 8 == 0 and 16-byte alignment (ldx=%d, K=%d)", ldx, K);
+  const int n_out = epilogue == LSK_EPI_SILU_MUL ? N / 2 : N;
+  if (ldy < n_out || ldy % 4 != 0 || !aligned(y, 8))
+    return fail(LSK_ERR_INVALID, "y needs ldy >= %d, ldy %% 4 == 0 and 8-byte alignment (ldy=%d)", n_out, ldy);
+  if (epilogue == LSK_EPI_RESIDUAL_ADD) {
+    if (residual == nullptr || ldr < N || !aligned(residual, 2))
+      return fail(LSK_ERR_INVALID, "residual add needs a residual [M][N] with ldr >= N (ldr=%d)", ldr);
+  } else if (residual != nullptr) {
+    return fail(LSK_ERR_INVALID, "residual given without the residual-add epilogue");
+  }
+  return LSK_OK;
 }
 
 }  // namespace
@@ -151,25 +177,7 @@ int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const voi
                     int ldy, int epilogue, const void* residual, int ldr, void* workspace, size_t ws_bytes,
                     void* hip_stream) {
   g_last_error.clear();
-  if (int st = check_shape(layout_id, N, K)) return st;
-  if (epilogue != LSK_EPI_NONE && epilogue != LSK_EPI_SILU_MUL && epilogue != LSK_EPI_RESIDUAL_ADD)
-    return fail(LSK_ERR_INVALID, "unknown epilogue %d", epilogue);
-  if ((epilogue == LSK_EPI_SILU_MUL) != (layout_id == LSK_LAYOUT_MFMA16X32_GATEUP))
-    return fail(LSK_ERR_INVALID, "the SiLU*up epilogue requires the interleaved gate_up layout and vice versa");
-  if (M < 1) return fail(LSK_ERR_INVALID, "M=%d must be >= 1", M);
-  if (w_packed == nullptr || x == nullptr || y == nullptr) return fail(LSK_ERR_INVALID, "null device pointer");
-  if (!aligned(w_packed, 16)) return fail(LSK_ERR_INVALID, "packed weights must be 16-byte aligned");
-  if (ldx < K || ldx % 8 != 0 || !aligned(x, 16))
-    return fail(LSK_ERR_INVALID, "x needs ldx >= K, ldx %% 8 == 0 and 16-byte alignment (ldx=%d, K=%d)", ldx, K);
-  const int n_out = epilogue == LSK_EPI_SILU_MUL ? N / 2 : N;
-  if (ldy < n_out || ldy % 4 != 0 || !aligned(y, 8))
-    return fail(LSK_ERR_INVALID, "y needs ldy >= %d, ldy %% 4 == 0 and 8-byte alignment (ldy=%d)", n_out, ldy);
-  if (epilogue == LSK_EPI_RESIDUAL_ADD) {
-    if (residual == nullptr || ldr < N || !aligned(residual, 2))
-      return fail(LSK_ERR_INVALID, "residual add needs a residual [M][N] with ldr >= N (ldr=%d)", ldr);
-  } else if (residual != nullptr) {
-    return fail(LSK_ERR_INVALID, "residual given without the residual-add epilogue");
-  }
+  if (int st = check_linear_args(w_packed, layout_id, N, K, x, M, ldx, y, ldy, epilogue, residual, ldr)) return st;
   auto stream = static_cast<hipStream_t>(hip_stream);
   const auto epi = static_cast<lsk::Epilogue>(epilogue);
   hipError_t err;
@@ -200,6 +208,23 @@ int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const voi
     }
   }
   if (err != hipSuccess) return hip_fail(err, "projection kernel launch");
+  return LSK_OK;
+}
+
+int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx,
+                            const void* norm_weight, float eps, void* y, int ldy, int epilogue,
+                            const void* residual, int ldr, void* hip_stream) {
+  g_last_error.clear();
+  if (int st = check_linear_args(w_packed, layout_id, N, K, x, M, ldx, y, ldy, epilogue, residual, ldr)) return st;
+  if (M > lsk::kDecodeMaxM)
+    return fail(LSK_ERR_INVALID, "the fused RMSNorm projection takes M=1..%d rows (M=%d)", lsk::kDecodeMaxM, M);
+  if (norm_weight == nullptr || !aligned(norm_weight, 16))
+    return fail(LSK_ERR_INVALID, "the RMSNorm weight [K] must be a 16-byte aligned device pointer");
+  if (!std::isfinite(eps) || eps < 0.f) return fail(LSK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
+  hipError_t err = lsk::launch_decode_rmsnorm_linear(w_packed, N, K, x, M, ldx, norm_weight, eps, y, ldy,
+                                                     static_cast<lsk::Epilogue>(epilogue), residual, ldr,
+                                                     static_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess) return hip_fail(err, "RMSNorm projection kernel launch");
   return LSK_OK;
 }
 

@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 
 #include <climits>
+#include <mutex>
 
 #include "lsk_internal.h"
 
@@ -126,6 +127,232 @@ __device__ __forceinline__ void accumulate_rows(f32x4_t (&acc)[RBW], const bf16x
   }
 }
 
+// ---------------------------------------------------------------- RMSNorm prologue
+//
+// y = epilogue(rms_norm(x) . W^T) with rms_norm(x)[m][k] =
+// bf16(x[m][k] * nw[k] * r[m]), r[m] = 1 / sqrt(sum_k x[m][k]^2 / K + eps),
+// in fp32 with one bf16 rounding -- torch's fused F.rms_norm over the hidden
+// dimension (src/leanstack/runtime/qwen_explicit.py:621-628, applied before
+// the QKV GEMV at :1255 and before the gate_up GEMV at :941) and the cuTile
+// bf16_rmsnorm_kernel (experiments/cutile/qwen_bf16_hot_kernels.py:39-49, its
+// torch reference at :52-57), which multiply in the order (x * r) * nw.
+// Each wave sums the squares of its own K slice; one LDS exchange gives every
+// lane the whole row's sum.
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Sum of the squares of a fragment's 8 values in fp32 (v_dot2c_f32_bf16:
+// the bf16 products are exact in fp32).
+__device__ __forceinline__ float sum_squares(bf16x8_t v) {
+  float s = 0.f;
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), __builtin_shufflevector(v, v, 0, 1), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), __builtin_shufflevector(v, v, 2, 3), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), __builtin_shufflevector(v, v, 4, 5), s, false);
+  s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), __builtin_shufflevector(v, v, 6, 7), s, false);
+  return s;
+}
+
+// Lanes 0..15 hold this wave's partial sum of squares of rows 0..15; returns
+// r[lane % 16] for active rows and 0 for padding columns, summing the waves'
+// partials in wave order.  Every wave must call it.
+template <int NW>
+__device__ __forceinline__ float row_inv_rms(float ss, int wave, int lane, int K, float eps, bool m_active) {
+  __shared__ float part[NW][16];
+  if (lane < 16) part[wave][lane] = ss;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) total += part[w][lane & 15];
+  return m_active ? 1.0f / sqrtf(total / static_cast<float>(K) + eps) : 0.f;
+}
+
+// bf16((x * nw) * r) of one fragment; `keep` clears padding columns.  The
+// product of two bf16 values is exact in fp32, so this is x * nw * r with two
+// roundings (fp32, then bf16); the reference's (x * r) * nw differs from it
+// by at most one fp32 rounding before the bf16 one.
+__device__ __forceinline__ bf16x8_t rms_scale(bf16x8_t xv, bf16x8_t nv, float r, unsigned keep) {
+  bf16x8_t o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = static_cast<__bf16>((static_cast<float>(xv[e]) * static_cast<float>(nv[e])) * r);
+  u32x4_t bits = __builtin_bit_cast(u32x4_t, o);
+  bits &= keep;
+  return __builtin_bit_cast(bf16x8_t, bits);
+}
+
+// The same from a chunk of x and its 8 norm weights as 4 packed pairs:
+// v_dot2c_f32_bf16 of an x pair with a weight pair whose other half is
+// masked to zero is the one exact product, so each value costs a mask, a dot
+// and a multiply.
+__device__ __forceinline__ bf16x8_t rms_scale_pairs(bf16x8_t xv, u32x4_t wv, float r) {
+  const u32x4_t xp = __builtin_bit_cast(u32x4_t, xv);
+  u32x4_t o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // Copy the elements out first: this compiler turns __builtin_bit_cast of
+    // a vector element with a loop index into a read of element 0.
+    const unsigned xe = xp[q], we = wv[q];
+    const bf16x2_t xq = __builtin_bit_cast(bf16x2_t, xe);
+    const float lo = __builtin_amdgcn_fdot2_f32_bf16(xq, __builtin_bit_cast(bf16x2_t, we & 0x0000ffffu), 0.f, false) * r;
+    const float hi = __builtin_amdgcn_fdot2_f32_bf16(xq, __builtin_bit_cast(bf16x2_t, we & 0xffff0000u), 0.f, false) * r;
+    o[q] = __builtin_bit_cast(unsigned, bf16x2_t{static_cast<__bf16>(lo), static_cast<__bf16>(hi)});
+  }
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+// Dynamic LDS of the single-round RMSNorm prologue: one area per wave.
+extern __shared__ __align__(16) unsigned char rms_lds[];
+
+// Bytes of one wave's area in the single-round RMSNorm prologue: the slice's
+// norm weights (U*4 chunks of 16 bytes), then the per-chunk sums of squares,
+// later overwritten by the M normalised rows of the slice (U * 32 values +
+// 8 of padding each).  At the end the wave's partial output tiles
+// (RBW x 1 KiB) go to the start of the area for the cross-wave sum.
+__host__ __device__ constexpr int rms_wave_bytes(int U, int NC, int M, int RBW) {
+  const int stage = U * 4 * 16 + (NC * 64 * 4 > M * (U * 32 + 8) * 2 ? NC * 64 * 4 : M * (U * 32 + 8) * 2);
+  return stage > RBW * 1024 ? stage : RBW * 1024;
+}
+
+// Single-round accumulate_rows with the RMSNorm prologue (K/32 == NW * U).
+// The wave's slice of x -- M rows x U*32 values, M*U*4 chunks of 8 -- is
+// spread densely over the lanes, NC chunks per lane, so no lane works for a
+// padding column.  Every activation and norm-weight chunk is loaded before
+// the weight tiles; the sums of squares, the exchange between waves and the
+// scaling run while the weights are in flight.  The normalised rows are
+// staged in this wave's LDS area and read back as B fragments.  Sums are
+// taken in a fixed order (chunks in K order within a wave, then waves in
+// order), so results are bitwise reproducible.
+template <int NW, int RBW, int U, int NC>
+__device__ __forceinline__ void accumulate_rows_rms_dense(f32x4_t (&acc)[RBW], const bf16x8_t* __restrict__ wt,
+                                                          const __bf16* __restrict__ x, int ldx,
+                                                          const bf16x8_t* __restrict__ nw, int M, int KT, int kb,
+                                                          int wave, int lane, float eps) {
+  constexpr int kRowChunks = U * 4;     // chunks of 8 values per row of the slice
+  constexpr int kRowStride = U * 32 + 8;  // bf16 per staged row: 16 rows start on 16 distinct bank quads
+  unsigned char* area = rms_lds + (size_t)wave * rms_wave_bytes(U, NC, M, RBW);
+  u32x4_t* nws = reinterpret_cast<u32x4_t*>(area);
+  float* ssq = reinterpret_cast<float*>(nws + kRowChunks);
+  __bf16* xs = reinterpret_cast<__bf16*>(nws + kRowChunks);
+  const int C = M * kRowChunks;
+  const int m = lane & 15;
+  const int g = lane >> 4;
+  const int mr = m < M ? m : M - 1;  // padding columns read row M-1: finite, and never stored
+
+  // Lanes past the last chunk reload it (in bounds); their results are dropped.
+  // Lanes 0..U*4-1 also load the slice's norm-weight chunks.
+  const bf16x8_t nwc = nw[kb * 4 + min(lane, kRowChunks - 1)];
+  bf16x8_t xd[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + 64 * i, C - 1);
+    const int mc = c / kRowChunks;
+    const int j = c - mc * kRowChunks;
+    xd[i] = *reinterpret_cast<const bf16x8_t*>(x + (size_t)mc * ldx + (kb * 4 + j) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  bf16x8_t wv[U][RBW];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kb + u) * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Every lane stores (lanes past the last chunk repeat chunk U*4-1, same
+  // value, same slot): a store under `lane < U*4` lets the compiler sink the
+  // load into that branch, behind the weight loads, and wait for all of them.
+  nws[min(lane, kRowChunks - 1)] = __builtin_bit_cast(u32x4_t, nwc);
+  // Straight-line stores (no branch per chunk): slots past C are never read.
+#pragma unroll
+  for (int i = 0; i < NC; ++i) ssq[lane + 64 * i] = sum_squares(xd[i]);
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRowChunks; ++j) ss += ssq[mr * kRowChunks + j];
+  // ssq and xs share the wave's area: these reads of ssq come before the
+  // wave's writes of xs in program order, and LDS serves a wave in order.
+  const float rr = row_inv_rms<NW>(ss, wave, lane, KT * kTileK, eps, m < M);
+
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane + 64 * i;
+    const int cc = min(c, C - 1);
+    const int mc = cc / kRowChunks;
+    const int j = cc - mc * kRowChunks;
+    const float rc = __shfl(rr, mc);  // lane mc < 16 holds r of row mc
+    const bf16x8_t o = rms_scale_pairs(xd[i], nws[j], rc);
+    // Lanes past the last chunk store the last chunk's own value again.
+    *reinterpret_cast<bf16x8_t*>(xs + mc * kRowStride + j * 8) = o;
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + mr * kRowStride + u * 32 + g * 8);
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+  }
+}
+
+// Round-based accumulate_rows with the RMSNorm prologue (any K): a first pass
+// over the wave's activation fragments (cache hits) gives r, then the rounds
+// run as in accumulate_rows with each fragment scaled before its multiply.
+// nrow: norm weight as 16-byte units, + g (the index pattern of xrow).
+template <int NW, int RBW>
+__device__ __forceinline__ void accumulate_rows_rms(f32x4_t (&acc)[RBW], const bf16x8_t* __restrict__ wt,
+                                                    const bf16x8_t* __restrict__ xrow,
+                                                    const bf16x8_t* __restrict__ nrow, bool m_active, int KT,
+                                                    int kb, int ke, int wave, int lane, float eps) {
+  const unsigned keep = m_active ? 0xffffffffu : 0u;
+  float ss = 0.f;
+  for (int kt = kb; kt < ke; ++kt) ss += sum_squares(xrow[kt * 4]);
+  // lanes m, m+16, m+32, m+48 hold the four K groups of row m
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  const float rr = row_inv_rms<NW>(ss, wave, lane, KT * kTileK, eps, m_active);
+  constexpr int R = 8 / RBW;
+  int kt = kb;
+  for (; kt + R <= ke; kt += R) {
+    bf16x8_t xv[R], nv[R];
+    bf16x8_t wv[R][RBW];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      xv[u] = xrow[(kt + u) * 4];
+      nv[u] = nrow[(kt + u) * 4];
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kt + u) * 64);
+    }
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const bf16x8_t xn = rms_scale(xv[u], nv[u], rr, keep);
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+    }
+  }
+  for (; kt < ke; ++kt) {
+    const bf16x8_t xn = rms_scale(xrow[kt * 4], nrow[kt * 4], rr, keep);
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) acc[r] = mfma16(load_weight_tile(wt + ((size_t)r * KT + kt) * 64), xn, acc[r]);
+  }
+}
+
+// The same with wave w's tiles at base + w * stride (w >= 1): its own area
+// of the RMSNorm prologue, which it has finished reading.
+template <int NW, int RBW>
+__device__ __forceinline__ bool reduce_waves_at(f32x4_t (&acc)[RBW], int wave, int lane, unsigned char* base,
+                                                int stride) {
+  if (wave > 0) {
+    f32x4_t* t = reinterpret_cast<f32x4_t*>(base + (size_t)wave * stride);
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) t[r * 64 + lane] = acc[r];
+  }
+  __syncthreads();
+  if (wave != 0) return false;
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    const f32x4_t* t = reinterpret_cast<const f32x4_t*>(base + (size_t)w * stride);
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) acc[r] += t[r * 64 + lane];
+  }
+  return true;
+}
+
 // Sum the NW per-wave partial tiles in wave order into wave 0's acc.
 // Returns false on every wave other than 0 (those are done).
 template <int NW, int RBW>
@@ -149,12 +376,16 @@ __device__ __forceinline__ bool reduce_waves(f32x4_t (&acc)[RBW], int wave, int 
   }
 }
 
-// y = epilogue(x . W^T) for M <= 16.  Grid: (NB / RBW) workgroups of NW waves;
+// y = epilogue(x . W^T) for M <= 16, or epilogue(rms_norm(x) . W^T) with
+// NORM != 0: NORM > 0 is the single-round prologue with NORM chunks per lane
+// (U > 0, dynamic LDS of NW * rms_wave_bytes(U, NORM, M, RBW) bytes), NORM < 0
+// the round-based one (U == 0).  Grid: (NB / RBW) workgroups of NW waves;
 // U > 0 requires K/32 == NW * U (single-round loads).
-template <int NW, int RBW, int EPI, int U>
+template <int NW, int RBW, int EPI, int U, int NORM>
 __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, __bf16* __restrict__ y,
-    int ldy, const __bf16* __restrict__ residual, int ldr, int M, int KT) {
+    int ldy, const __bf16* __restrict__ residual, int ldr, int M, int KT, const __bf16* __restrict__ norm_w,
+    float eps) {
   static_assert(EPI != static_cast<int>(Epilogue::kSiluMul) || RBW == 2,
                 "SiLU*up pairs one gate and one up row-block per workgroup");
   const int lane = threadIdx.x & 63;
@@ -172,9 +403,25 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
-  accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
+  static_assert(NORM <= 0 || U > 0, "the dense RMSNorm prologue is single-round");
+  static_assert(NORM >= 0 || U == 0, "the per-lane RMSNorm prologue is round-based");
+  if constexpr (NORM > 0) {
+    accumulate_rows_rms_dense<NW, RBW, U, NORM>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w), M, KT,
+                                                kb, wave, lane, eps);
+  } else if constexpr (NORM < 0) {
+    const bf16x8_t* nrow = reinterpret_cast<const bf16x8_t*>(norm_w) + g;
+    accumulate_rows_rms<NW, RBW>(acc, wt, xrow, nrow, m_active, KT, kb, ke, wave, lane, eps);
+  } else {
+    (void)norm_w;
+    (void)eps;
+    accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
+  }
 
-  if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
+  if constexpr (NORM > 0) {
+    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NORM, M, RBW))) return;
+  } else {
+    if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
+  }
   if (!m_active) return;
 
   // Lane (g, m) holds output rows 4g..4g+3 of each row-block for column m.
@@ -316,12 +563,43 @@ __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const
 constexpr int kLmHeadWaves = 8;
 constexpr int kLmHeadRBW = 2;
 
-template <int NW, int RBW, int EPI, int U>
-hipError_t launch_decode_cfg(const void* w, int NB, int KT, const void* x, int M, int ldx, void* y,
-                             int ldy, const void* residual, int ldr, hipStream_t stream) {
-  decode_linear_kernel<NW, RBW, EPI, U><<<dim3(NB / RBW), dim3(NW * 64), 0, stream>>>(
-      static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
-      static_cast<const __bf16*>(residual), ldr, M, KT);
+// Launch arguments of one decode / verify projection.
+struct DecodeArgs {
+  const void* w;
+  int NB, KT;
+  const void* x;
+  int M, ldx;
+  void* y;
+  int ldy;
+  const void* residual;
+  int ldr;
+  const void* norm_w;  // RMSNorm weight [K], or null
+  float eps;
+};
+
+// Dynamic LDS a launch may use without raising the kernel's limit first.
+constexpr size_t kDefaultDynamicLds = 64 * 1024;
+
+template <int NW, int RBW, int EPI, int U, int NORM>
+hipError_t launch_decode_cfg(const DecodeArgs& a, hipStream_t stream) {
+  auto* kernel = decode_linear_kernel<NW, RBW, EPI, U, NORM>;
+  size_t lds = 0;
+  if constexpr (NORM > 0) {
+    lds = (size_t)NW * rms_wave_bytes(U, NORM, a.M, RBW);
+    if (lds > kDefaultDynamicLds) {
+      // Raised once per kernel, to what M = 16 needs.
+      static std::once_flag once;
+      static hipError_t raised = hipSuccess;
+      std::call_once(once, [&] {
+        raised = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     NW * rms_wave_bytes(U, NORM, kDecodeMaxM, RBW));
+      });
+      if (raised != hipSuccess) return raised;
+    }
+  }
+  kernel<<<dim3(a.NB / RBW), dim3(NW * 64), lds, stream>>>(
+      static_cast<const bf16x8_t*>(a.w), static_cast<const __bf16*>(a.x), a.ldx, static_cast<__bf16*>(a.y), a.ldy,
+      static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT, static_cast<const __bf16*>(a.norm_w), a.eps);
   return hipGetLastError();
 }
 
@@ -330,43 +608,68 @@ hipError_t launch_decode_cfg(const void* w, int NB, int KT, const void* x, int M
 // 304 -> 16 x 19, each measured faster than the alternatives on MI355X); any
 // other K runs the round-based variant.
 template <int RBW, int EPI>
-hipError_t launch_decode_shape(const void* w, int NB, int KT, const void* x, int M, int ldx, void* y, int ldy,
-                               const void* residual, int ldr, hipStream_t stream) {
-  switch (KT) {
+hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
+  switch (a.KT) {
     case 80:
       // 16 waves x 5 k-tiles, for the single row-block (QKV) and the gate/up
       // pair alike: measured 4.5 % / 3.2 % faster than 8 waves x 10 (whose
       // gate/up form needs 96 VGPRs and leaves 96 of 608 workgroups for a
       // second wave) and than the round-based loop.
-      return launch_decode_cfg<16, RBW, EPI, 5>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      return launch_decode_cfg<16, RBW, EPI, 5, 0>(a, stream);
     case 128:
-      if constexpr (RBW == 1) return launch_decode_cfg<8, RBW, EPI, 16>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      if constexpr (RBW == 1) return launch_decode_cfg<8, RBW, EPI, 16, 0>(a, stream);
       break;
     case 304:
-      if constexpr (RBW == 1) return launch_decode_cfg<16, RBW, EPI, 19>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+      if constexpr (RBW == 1) return launch_decode_cfg<16, RBW, EPI, 19, 0>(a, stream);
       break;
     default:
       break;
   }
-  if (KT >= 256) return launch_decode_cfg<16, RBW, EPI, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
-  return launch_decode_cfg<8, RBW, EPI, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
+  if (a.KT >= 256) return launch_decode_cfg<16, RBW, EPI, 0, 0>(a, stream);
+  return launch_decode_cfg<8, RBW, EPI, 0, 0>(a, stream);
+}
+
+// The same with the RMSNorm prologue.  K/32 = 80 (the Qwen3-4B hidden size
+// the norms act on) runs single-round with the dense prologue, its chunks
+// per lane (M * 20 chunks over 64 lanes) picked from M; any other K runs
+// the round-based prologue.
+template <int RBW, int EPI>
+hipError_t launch_rms_shape(const DecodeArgs& a, hipStream_t stream) {
+  if (a.KT == 80) {
+    if (a.M <= 3) return launch_decode_cfg<16, RBW, EPI, 5, 1>(a, stream);
+    if (a.M <= 9) return launch_decode_cfg<16, RBW, EPI, 5, 3>(a, stream);
+    return launch_decode_cfg<16, RBW, EPI, 5, 5>(a, stream);
+  }
+  if (a.KT >= 256) return launch_decode_cfg<16, RBW, EPI, 0, -1>(a, stream);
+  return launch_decode_cfg<8, RBW, EPI, 0, -1>(a, stream);
+}
+
+template <bool NORM>
+hipError_t launch_decode_epi(const DecodeArgs& a, Epilogue epi, hipStream_t stream) {
+  switch (epi) {
+    case Epilogue::kSiluMul:
+      return NORM ? launch_rms_shape<2, 1>(a, stream) : launch_decode_shape<2, 1>(a, stream);
+    case Epilogue::kResidualAdd:
+      return NORM ? launch_rms_shape<1, 2>(a, stream) : launch_decode_shape<1, 2>(a, stream);
+    case Epilogue::kNone:
+    default:
+      return NORM ? launch_rms_shape<1, 0>(a, stream) : launch_decode_shape<1, 0>(a, stream);
+  }
 }
 
 }  // namespace
 
 hipError_t launch_decode_linear(const void* w, int N, int K, const void* x, int M, int ldx, void* y,
                                 int ldy, Epilogue epi, const void* residual, int ldr, hipStream_t stream) {
-  const int NB = N / kTileRows;
-  const int KT = K / kTileK;
-  switch (epi) {
-    case Epilogue::kSiluMul:
-      return launch_decode_shape<2, 1>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
-    case Epilogue::kResidualAdd:
-      return launch_decode_shape<1, 2>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
-    case Epilogue::kNone:
-    default:
-      return launch_decode_shape<1, 0>(w, NB, KT, x, M, ldx, y, ldy, residual, ldr, stream);
-  }
+  const DecodeArgs a{w, N / kTileRows, K / kTileK, x, M, ldx, y, ldy, residual, ldr, nullptr, 0.f};
+  return launch_decode_epi<false>(a, epi, stream);
+}
+
+hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void* x, int M, int ldx,
+                                        const void* norm_w, float eps, void* y, int ldy, Epilogue epi,
+                                        const void* residual, int ldr, hipStream_t stream) {
+  const DecodeArgs a{w, N / kTileRows, K / kTileK, x, M, ldx, y, ldy, residual, ldr, norm_w, eps};
+  return launch_decode_epi<true>(a, epi, stream);
 }
 
 int lm_head_partials(int V) { return (V / kTileRows) / kLmHeadRBW; }

@@ -93,6 +93,12 @@ hipError_t launch_decode_linear(const void* w, int N, int K, const void* x, int 
                                 void* y, int ldy, Epilogue epi, const void* residual, int ldr,
                                 hipStream_t stream);
 
+// The same with an RMSNorm of each x row in front of the projection
+// (norm_w: bf16 [K], 16-byte aligned).
+hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void* x, int M, int ldx,
+                                        const void* norm_w, float eps, void* y, int ldy, Epilogue epi,
+                                        const void* residual, int ldr, hipStream_t stream);
+
 // Number of workgroups (= argmax partials per row) the lm_head kernel uses.
 int lm_head_partials(int V);
 

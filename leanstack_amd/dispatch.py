@@ -17,7 +17,11 @@ Differences from the reference, on purpose:
     torch when its kernel raises (:1820-1832); here a missing library or a
     rejected argument always raises.
   - residual adds that follow a projection (:820, :831, :949) are fused into
-    that projection's epilogue, with the same bf16 rounding.
+    that projection's epilogue, with the same bf16 rounding;
+  - for decode and verify rows (M <= 16) the RMSNorm in front of gate_up
+    (:821-827, :941) runs inside the gate_up kernel (kernels.rmsnorm_linear,
+    one bf16 rounding as F.rms_norm); _semantic_input_norm_attention_qkv_vector
+    offers the same for input_layernorm + QKV (:1255 then :787).
 """
 
 from __future__ import annotations
@@ -88,6 +92,14 @@ def _check_gate_dim(gate_up_proj_weight: PackedWeight, gate_proj_out_dim: int) -
 # ------------------------------------------------------------ projections
 
 
+def _norm_gate_up(hidden_states, norm_weight, eps, gu_w: PackedWeight):
+    """SiLU(gate)*up of rms_norm(hidden_states): fused into the gate_up kernel
+    for decode / verify rows, F.rms_norm then the GEMM for prefill rows."""
+    if hidden_states.numel() // gu_w.k <= _lib.DECODE_MAX_M:
+        return kernels.rmsnorm_linear(hidden_states, norm_weight, eps, gu_w, epilogue=_lib.EPI_SILU_MUL)
+    return kernels.linear(qwen_rmsnorm(hidden_states, norm_weight, eps), gu_w, epilogue=_lib.EPI_SILU_MUL)
+
+
 def _semantic_attention_qkv(hidden_states, qkv_proj_weight, q_proj_out_dim, k_proj_out_dim, num_attention_heads,
                             num_key_value_heads, head_dim, q_norm_weight, k_norm_weight, cos, sin, rms_norm_eps):
     """M>1 fused QKV (qwen_explicit.py:733-770): [B,T,H] -> q [B,nq,T,d], k/v [B,nkv,T,d]."""
@@ -113,6 +125,13 @@ def _semantic_attention_qkv_vector(hidden_states, qkv_proj_weight, q_proj_out_di
     """M=1 fused QKV GEMV (qwen_explicit.py:773-806): hidden [H] -> q [1,nq,1,d], k/v [1,nkv,1,d]."""
     w = _require_packed(qkv_proj_weight, "qkv_proj_weight")
     qkv_states = kernels.linear(hidden_states.view(1, -1), w).view(-1)
+    return _qkv_heads_vector(qkv_states, q_proj_out_dim, k_proj_out_dim, num_attention_heads, num_key_value_heads,
+                             head_dim, q_norm_weight, k_norm_weight, cos, sin, rms_norm_eps)
+
+
+def _qkv_heads_vector(qkv_states, q_proj_out_dim, k_proj_out_dim, num_attention_heads, num_key_value_heads,
+                      head_dim, q_norm_weight, k_norm_weight, cos, sin, rms_norm_eps):
+    """Split a [qkv] row into heads, q/k norm and RoPE (qwen_explicit.py:788-806)."""
     query_states, key_states, value_states = torch.split(
         qkv_states, (q_proj_out_dim, k_proj_out_dim, k_proj_out_dim), dim=0)
     query_states = F.rms_norm(query_states.view(1, num_attention_heads, head_dim), normalized_shape=(head_dim,),
@@ -121,6 +140,19 @@ def _semantic_attention_qkv_vector(hidden_states, qkv_proj_weight, q_proj_out_di
                             weight=k_norm_weight, eps=rms_norm_eps).view(1, num_key_value_heads, 1, head_dim)
     value_states = value_states.view(1, num_key_value_heads, 1, head_dim)
     return qwen_apply_rotary_pos_emb(query_states, key_states, cos, sin) + (value_states,)
+
+
+def _semantic_input_norm_attention_qkv_vector(residual, input_layernorm_weight, qkv_proj_weight, q_proj_out_dim,
+                                              k_proj_out_dim, num_attention_heads, num_key_value_heads, head_dim,
+                                              q_norm_weight, k_norm_weight, cos, sin, rms_norm_eps):
+    """qwen_rmsnorm_vector(residual, input_layernorm_weight) followed by
+    _semantic_attention_qkv_vector (qwen_explicit.py:1255, then :773-806), with
+    the RMSNorm computed inside the QKV kernel: no normalised copy of the
+    hidden state is written.  Returns q [1,nq,1,d], k/v [1,nkv,1,d]."""
+    w = _require_packed(qkv_proj_weight, "qkv_proj_weight")
+    qkv_states = kernels.rmsnorm_linear(residual.reshape(1, -1), input_layernorm_weight, rms_norm_eps, w).view(-1)
+    return _qkv_heads_vector(qkv_states, q_proj_out_dim, k_proj_out_dim, num_attention_heads, num_key_value_heads,
+                             head_dim, q_norm_weight, k_norm_weight, cos, sin, rms_norm_eps)
 
 
 def _semantic_post_attention_mlp(attention_output, residual, o_proj_weight, post_attention_layernorm_weight,
@@ -132,10 +164,8 @@ def _semantic_post_attention_mlp(attention_output, residual, o_proj_weight, post
     d_w = _require_packed(down_proj_weight, "down_proj_weight")
     _check_gate_dim(gu_w, gate_proj_out_dim)
     hidden_states = kernels.linear(attention_output, o_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=residual)
-    residual = hidden_states
-    hidden_states = qwen_rmsnorm(hidden_states, post_attention_layernorm_weight, rms_norm_eps)
-    act = kernels.linear(hidden_states, gu_w, epilogue=_lib.EPI_SILU_MUL)
-    return kernels.linear(act, d_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=residual)
+    act = _norm_gate_up(hidden_states, post_attention_layernorm_weight, rms_norm_eps, gu_w)
+    return kernels.linear(act, d_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=hidden_states)
 
 
 def _semantic_mlp_epilogue(hidden_states, post_attention_layernorm_weight, gate_up_proj_weight, gate_proj_out_dim,
@@ -144,8 +174,7 @@ def _semantic_mlp_epilogue(hidden_states, post_attention_layernorm_weight, gate_
     gu_w = _require_packed(gate_up_proj_weight, "gate_up_proj_weight", _lib.LAYOUT_MFMA16X32_GATEUP)
     d_w = _require_packed(down_proj_weight, "down_proj_weight")
     _check_gate_dim(gu_w, gate_proj_out_dim)
-    normed = qwen_rmsnorm(hidden_states, post_attention_layernorm_weight, rms_norm_eps)
-    act = kernels.linear(normed, gu_w, epilogue=_lib.EPI_SILU_MUL)
+    act = _norm_gate_up(hidden_states, post_attention_layernorm_weight, rms_norm_eps, gu_w)
     return kernels.linear(act, d_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=hidden_states)
 
 
@@ -156,8 +185,8 @@ def _semantic_mlp_epilogue_vector(hidden_states, post_attention_layernorm_weight
     d_w = _require_packed(down_proj_weight, "down_proj_weight")
     _check_gate_dim(gu_w, gate_proj_out_dim)
     residual = hidden_states.reshape(1, -1)
-    normed = qwen_rmsnorm_vector(hidden_states, post_attention_layernorm_weight, rms_norm_eps)
-    act = kernels.linear(normed.view(1, -1), gu_w, epilogue=_lib.EPI_SILU_MUL)
+    act = kernels.rmsnorm_linear(residual, post_attention_layernorm_weight, rms_norm_eps, gu_w,
+                                 epilogue=_lib.EPI_SILU_MUL)
     return kernels.linear(act, d_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=residual).view(-1)
 
 

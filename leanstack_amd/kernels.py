@@ -114,6 +114,48 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
     return out
 
 
+def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weight: PackedWeight, *,
+                   epilogue: int = _lib.EPI_NONE, residual: torch.Tensor | None = None,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[..., N'] = epilogue(rms_norm(x) . W^T) for 1..16 rows of x, the
+    RMSNorm (F.rms_norm over the last dim with `norm_weight` and `eps`, one
+    bf16 rounding) computed inside the projection kernel."""
+    if not isinstance(weight, PackedWeight):
+        raise ValueError("weight must be a PackedWeight (pack it with leanstack_amd.layout / leanserve)")
+    lib = _lib.load()
+    _require_device(x, "x")
+    _require_device(weight.data, "weight")
+    _require_device(norm_weight, "norm_weight")
+    x2, m, ldx = _rows(x, weight.k, "x")
+    nw = norm_weight.reshape(-1)
+    if nw.dtype != torch.bfloat16 or nw.numel() != weight.k:
+        raise ValueError(f"norm_weight must be a bfloat16 [{weight.k}] tensor, got {nw.dtype} {tuple(norm_weight.shape)}")
+    if nw.stride(0) != 1 or nw.data_ptr() % 16:
+        nw = nw.contiguous() if nw.stride(0) != 1 else nw.clone()
+    n_out = weight.n // 2 if epilogue == _lib.EPI_SILU_MUL else weight.n
+    lead = x.shape[:-1]
+    if out is None:
+        out = torch.empty((*lead, n_out), device=x.device, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bfloat16 [..., {n_out}] tensor")
+    res_ptr, ldr = None, 0
+    if residual is not None:
+        _require_device(residual, "residual")
+        r2, rm, ldr = _rows(residual, weight.n, "residual")
+        if rm != m:
+            raise ValueError(f"residual has {rm} rows, x has {m}")
+        res_ptr = r2.data_ptr()
+    status = lib.lsk_rmsnorm_linear_bf16(
+        weight.data.data_ptr(), weight.layout, weight.n, weight.k,
+        x2.data_ptr(), m, ldx,
+        nw.data_ptr(), float(eps),
+        out.data_ptr(), n_out,
+        epilogue, res_ptr, ldr, stream_handle(),
+    )
+    _lib.check(status, "lsk_rmsnorm_linear_bf16")
+    return out
+
+
 class LmHeadWorkspace:
     """Device workspace of the two-stage argmax, sized once per (M, V, K)."""
 

@@ -49,6 +49,11 @@ class DecodeLinearStack:
                 "gate_up": torch.randn((n, max_rows, h), generator=gen, device=device).to(torch.bfloat16),
             }
         self.x_qkv, self.x_o, self.x_gu = inputs["qkv"], inputs["o"], inputs["gate_up"]
+        # input_layernorm / post_attention_layernorm weights of each layer
+        # (for the step with its RMSNorms, launch_with_norms)
+        gen_n = torch.Generator(device=device).manual_seed(2)
+        self.norm_w = (1.0 + 0.1 * torch.randn((n, 2, h), generator=gen_n, device=device)).to(torch.bfloat16)
+        self.eps = geometry.rms_norm_eps
         self.y_qkv = torch.empty((max_rows, qkv), device=device, dtype=torch.bfloat16)
         self.y_o = torch.empty((max_rows, h), device=device, dtype=torch.bfloat16)
         self.act = torch.empty((max_rows, i), device=device, dtype=torch.bfloat16)
@@ -63,6 +68,30 @@ class DecodeLinearStack:
             kernels.linear(self.x_qkv[l, :m], p.qkv, out=self.y_qkv[:m])
             kernels.linear(self.x_o[l, :m], p.o, out=self.y_o[:m])
             kernels.linear(self.x_gu[l, :m], p.gate_up, epilogue=_lib.EPI_SILU_MUL, out=self.act[:m])
+            kernels.linear(self.act[:m], p.down, out=self.y_down[:m])
+
+    def launch_with_norms(self, m: int, fused: bool) -> None:
+        """The step with the two RMSNorms of each layer in front of QKV
+        (input_layernorm, qwen_explicit.py:1255) and gate_up
+        (post_attention_layernorm, :941): inside those projections' kernels
+        when `fused`, else as F.rms_norm launches ahead of them."""
+        if not 1 <= m <= self.max_rows:
+            raise ValueError(f"m={m} outside 1..{self.max_rows}")
+        h = self.g.hidden_size
+        for l, p in enumerate(self.layers):
+            ln_in, ln_post = self.norm_w[l, 0], self.norm_w[l, 1]
+            if fused:
+                kernels.rmsnorm_linear(self.x_qkv[l, :m], ln_in, self.eps, p.qkv, out=self.y_qkv[:m])
+            else:
+                normed = torch.nn.functional.rms_norm(self.x_qkv[l, :m], (h,), ln_in, self.eps)
+                kernels.linear(normed, p.qkv, out=self.y_qkv[:m])
+            kernels.linear(self.x_o[l, :m], p.o, out=self.y_o[:m])
+            if fused:
+                kernels.rmsnorm_linear(self.x_gu[l, :m], ln_post, self.eps, p.gate_up, epilogue=_lib.EPI_SILU_MUL,
+                                       out=self.act[:m])
+            else:
+                normed = torch.nn.functional.rms_norm(self.x_gu[l, :m], (h,), ln_post, self.eps)
+                kernels.linear(normed, p.gate_up, epilogue=_lib.EPI_SILU_MUL, out=self.act[:m])
             kernels.linear(self.act[:m], p.down, out=self.y_down[:m])
 
     def launch_projection(self, name: str, m: int) -> None:

@@ -63,6 +63,31 @@ def test_linear_rejects_before_launch(kwargs, code):
         _lib.check(status, "lsk_linear_bf16")
 
 
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(layout=9), _lib.ERR_LAYOUT),
+    (dict(k=2576), _lib.ERR_INVALID),        # K not a multiple of 32
+    (dict(m=0), _lib.ERR_INVALID),
+    (dict(m=17), _lib.ERR_INVALID),          # decode / verify rows only
+    (dict(nw=0), _lib.ERR_INVALID),          # no norm weight
+    (dict(nw=FAKE + 8), _lib.ERR_INVALID),   # norm weight misaligned
+    (dict(eps=-1e-6), _lib.ERR_INVALID),
+    (dict(eps=float("nan")), _lib.ERR_INVALID),
+    (dict(eps=float("inf")), _lib.ERR_INVALID),
+    (dict(epi=1), _lib.ERR_INVALID),         # SiLU needs the gate_up layout
+    (dict(layout=2), _lib.ERR_INVALID),      # gate_up layout needs the SiLU epilogue
+    (dict(x=FAKE + 2), _lib.ERR_INVALID),
+    (dict(ldy=6140), _lib.ERR_INVALID),
+])
+def test_rmsnorm_linear_rejects_before_launch(kwargs, code):
+    a = dict(w=FAKE, layout=1, n=6144, k=2560, x=FAKE, m=1, ldx=2560, nw=FAKE, eps=1e-6, y=FAKE, ldy=6144, epi=0)
+    a.update(kwargs)
+    lib = _lib.load()
+    status = lib.lsk_rmsnorm_linear_bf16(a["w"], a["layout"], a["n"], a["k"], a["x"], a["m"], a["ldx"],
+                                         a["nw"] or None, a["eps"], a["y"], a["ldy"], a["epi"], None, 0, None)
+    assert status == code, _lib.last_error()
+    assert _lib.last_error()
+
+
 def test_lm_head_rejects_before_launch():
     lib = _lib.load()
     ok = dict(V=151936, K=2560, M=1)

@@ -69,6 +69,30 @@ def test_attention_qkv_vector(gpu):
     assert_parity(v.cpu(), vs.view(1, 8, 1, 128), "v")
 
 
+def test_input_norm_attention_qkv_vector(gpu):
+    """input_layernorm + QKV in one kernel equals qwen_rmsnorm_vector (:1255)
+    followed by the QKV path (:773-806) on the oracle."""
+    w = weight(G.qkv_dim, G.hidden_size, seed=11)
+    resid = (activations(1, G.hidden_size, seed=12).float() * 6.0).to(torch.bfloat16).view(-1)
+    ln = seeded_normal((G.hidden_size,), 0.2, 13) + 1
+    qn = seeded_normal((G.head_dim,), 0.1, 14) + 1
+    kn = seeded_normal((G.head_dim,), 0.1, 15) + 1
+    cos, sin = _cos_sin(8)
+    cos, sin = cos[:, 3:4], sin[:, 3:4]
+    q, k, v = dispatch._semantic_input_norm_attention_qkv_vector(
+        resid.to(DEV), ln.to(DEV), _pw(w), G.q_dim, G.kv_dim, G.num_attention_heads, G.num_key_value_heads,
+        G.head_dim, qn.to(DEV), kn.to(DEV), cos.to(DEV), sin.to(DEV), G.rms_norm_eps)
+    h = ref.rmsnorm(resid.view(1, -1), ln, G.rms_norm_eps).view(-1)
+    qkv = ref.mv(w, h)
+    qs, ks, vs = torch.split(qkv, (G.q_dim, G.kv_dim, G.kv_dim))
+    qs = F.rms_norm(qs.view(1, 32, 128), (128,), qn, G.rms_norm_eps).view(1, 32, 1, 128)
+    ks = F.rms_norm(ks.view(1, 8, 128), (128,), kn, G.rms_norm_eps).view(1, 8, 1, 128)
+    eq, ek = _rope_cpu(qs, ks, cos, sin)
+    assert_parity(q.cpu(), eq, "q")
+    assert_parity(k.cpu(), ek, "k")
+    assert_parity(v.cpu(), vs.view(1, 8, 1, 128), "v")
+
+
 def test_attention_qkv_batched(gpu):
     t = 5
     w = weight(G.qkv_dim, G.hidden_size, seed=11)

@@ -177,3 +177,53 @@ def test_mlp_epilogue_vector_composes_the_reference_steps():
     assert torch.allclose(out.double(), expect, rtol=3e-2, atol=3e-2)
     # the residual is really added: dropping it moves the result by |h|
     assert (out.double() - (expect - hf)).abs().max() > 0.5
+
+
+def test_rmsnorm_closed_forms():
+    """rms_norm of a constant row c with eps = 0 is sign(c) * w exactly (r = 1/|c|
+    for a power-of-two c), and eps enters under the square root: with
+    x = 1 and eps = 3 the row is scaled by 1/2."""
+    k = 2560
+    w = torch.tensor(np.random.default_rng(12).standard_normal(k), dtype=torch.float32).to(torch.bfloat16)
+    for c in (0.25, 1.0, -8.0, 64.0):
+        x = torch.full((1, k), c, dtype=torch.bfloat16)
+        out = ref.rmsnorm(x, w, 0.0)
+        assert torch.equal(out[0], (w.float() * np.sign(c)).to(torch.bfloat16))
+    out = ref.rmsnorm(torch.ones(1, k, dtype=torch.bfloat16), w, 3.0)
+    assert torch.equal(out[0], (w.float() * 0.5).to(torch.bfloat16))
+
+
+def test_rmsnorm_power_of_two_scale_invariance():
+    """With eps = 0, scaling a row by 2^j changes neither r * x nor the output
+    (a wrong exponent of the mean, or a missing square, breaks this)."""
+    rng = np.random.default_rng(13)
+    x = torch.tensor(rng.standard_normal((3, 2560)), dtype=torch.float32).to(torch.bfloat16)
+    w = torch.tensor(1 + 0.2 * rng.standard_normal(2560), dtype=torch.float32).to(torch.bfloat16)
+    base = ref.rmsnorm(x, w, 0.0)
+    for j in (-3, 2, 5):
+        assert torch.equal(ref.rmsnorm(x * (2.0 ** j), w, 0.0), base)
+
+
+def test_rmsnorm_matches_float64_one_rounding():
+    """Each output is the float64 value (x * r) * w rounded once to bf16, to
+    within one bf16 step where the fp32 evaluation lands next to a rounding
+    boundary; the two-rounding form bf16(bf16(x * r) * w) of the composite
+    fallback (qwen_explicit.py:629-633) differs from it on many elements,
+    so the chain is pinned as the single rounding of the cuTile kernel and
+    its torch reference (experiments/cutile/qwen_bf16_hot_kernels.py:45-57)."""
+    rng = np.random.default_rng(14)
+    k = 2560
+    xb = brute.f32_to_bf16_bits((rng.standard_normal((4, k)) * np.array([[0.1], [1.0], [7.0], [300.0]]))
+                                .astype(np.float32))
+    wb = brute.f32_to_bf16_bits((1 + 0.3 * rng.standard_normal(k)).astype(np.float32))
+    eps = 1e-6
+    x64, w64 = brute.bf16_bits_to_f64(xb), brute.bf16_bits_to_f64(wb)
+    r64 = 1.0 / np.sqrt((x64 * x64).mean(axis=1, keepdims=True) + eps)
+    y64 = x64 * r64 * w64
+    got = ref.rmsnorm(from_bits(xb), from_bits(wb), eps).double().numpy()
+    step = brute.bf16_ulp(y64)
+    assert np.all(np.abs(got - y64) <= step * (0.5 + 2e-3) + 1e-30)
+    exact = np.mean(got == brute.round_bf16(y64))
+    assert exact > 0.995
+    two = brute.round_bf16(brute.round_bf16(x64 * r64) * w64)
+    assert np.mean(got != two) > 0.1
