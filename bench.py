@@ -137,7 +137,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc", action="store_true",
                     help="short run for hardware-counter profiling: a 1 GiB copy of known size, then each "
-                         "projection kind once per layer and the lm_head once, no graphs")
+                         "projection kind once per layer, the QKV and gate_up kernels with the RMSNorm prologue "
+                         "once per layer, and the lm_head once, no graphs")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
                          "M = 2048 and 8192, three launches each, no graphs")
@@ -193,6 +194,12 @@ def main() -> int:
         torch.cuda.synchronize()
         for name in G.projections():
             stack.launch_projection(name, 1)
+        # the QKV and gate_up kernels with the RMSNorm prologue, once per layer each
+        for l, p in enumerate(layers):
+            kernels.rmsnorm_linear(stack.x_qkv[l, :1], stack.norm_w[l, 0], stack.eps, p.qkv, out=stack.y_qkv[:1])
+        for l, p in enumerate(layers):
+            kernels.rmsnorm_linear(stack.x_gu[l, :1], stack.norm_w[l, 1], stack.eps, p.gate_up,
+                                   epilogue=_lib.EPI_SILU_MUL, out=stack.act[:1])
         hidden = torch.randn((1, G.hidden_size), generator=gen, device=dev).to(torch.bfloat16)
         kernels.lm_head_argmax(hidden, lm_head)
         torch.cuda.synchronize()
@@ -278,7 +285,7 @@ def main() -> int:
     else:
         # Dominant kernel of the launch graph: the fused gate_up + SiLU*up
         # decode kernel (49% of the step's bytes), timed over 36 launches.
-        roof_kernel = "decode_linear_kernel<16,2,1,5> (gate_up 19456x2560 + silu*up, M=1)"
+        roof_kernel = "decode_linear_kernel<16,2,1,5,0> (gate_up 19456x2560 + silu*up, M=1)"
         roof_bytes = G.projection_bytes("gate_up_proj", 1)
         achieved = roof_bytes / (per_kernel["gate_up_proj"]["us_per_launch"] * 1e-6) / 1e9
 
