@@ -11,7 +11,8 @@ activations read + outputs written) / step time, in GB/s.
 
 Also reported (under "detail"): the verify sweep M = 1, 2, 4, 8 over the same
 stack, the step with the two RMSNorms of each layer (fused into the QKV and
-gate_up kernels, or as separate F.rms_norm launches), each projection kind's
+gate_up kernels, or as separate F.rms_norm launches), a whole decode token with
+attention over 320 and 4095 cached rows (every layer HIP), each projection kind's
 per-launch time, the tied lm_head + argmax at M = 1..8, and the prefill GEMMs
 at M = 512, 2048, 8192 in TFLOP/s.
 
@@ -154,7 +155,7 @@ def main() -> int:
     from leanstack_amd.build import LIBRARY, build_library
     from leanstack_amd.geometry import QWEN3_4B as G
     from leanstack_amd.leanserve import ResidentArena, build_resident_buffer_plan, layer_entry_names
-    from leanstack_amd.stack import DecodeLinearStack, LayerProjections
+    from leanstack_amd.stack import DecodeLinearStack, DecodeStep, LayerProjections
 
     if not LIBRARY.exists():
         build_library()
@@ -263,6 +264,28 @@ def main() -> int:
         norm_steps[m] = row
         log(f"step with RMSNorms M={m}: fused {row['fused']} us, separate {row['separate_rms_norm']} us, "
             f"projections only {row['projections_only']} us")
+
+    # --- a whole decode token with attention, every layer HIP ----------------
+    # input norm + QKV, attention (q/k norms, RoPE, cache append, GQA over the
+    # cached rows), o_proj + residual, post norm + gate_up, down + residual,
+    # then the final norm and the lm_head argmax; cache rows random.
+    token_steps = {}
+    n_l, n_kv, hd = G.num_hidden_layers, G.num_key_value_heads, G.head_dim
+    kv_rows = 4096
+    k_cache = torch.randn((n_l, n_kv, kv_rows, hd), generator=gen, device=dev).to(torch.bfloat16)
+    v_cache = torch.randn((n_l, n_kv, kv_rows, hd), generator=gen, device=dev).to(torch.bfloat16)
+    norms = (1 + 0.1 * torch.randn((n_l, 2, G.hidden_size), generator=gen, device=dev)).to(torch.bfloat16)
+    qk_norms = (1 + 0.1 * torch.randn((n_l, 2, hd), generator=gen, device=dev)).to(torch.bfloat16)
+    final_norm = (1 + 0.1 * torch.randn((G.hidden_size,), generator=gen, device=dev)).to(torch.bfloat16)
+    token_step = DecodeStep(layers, norms, qk_norms, final_norm, lm_head, G, k_cache, v_cache, dev)
+    token_step.hidden[0].copy_(torch.randn((1, G.hidden_size), generator=gen, device=dev).to(torch.bfloat16))
+    for pos in (320, kv_rows - 1):
+        graph = stack.capture(lambda pos=pos: token_step.launch(pos))
+        ms = time_graph(torch, graph, steps, warmup)
+        token_steps[pos] = {"us": round(ms * 1e3, 1), "tokens_per_s": round(1e3 / ms, 1)}
+        log(f"decode token with attention over {pos} cached rows: {ms * 1e3:.1f} us ({1e3 / ms:.0f} tokens/s)")
+        del graph
+    del token_step, k_cache, v_cache
 
     # --- per projection kind: 36 launches of one kind per replay ------------
     per_kernel = {}
@@ -374,6 +397,7 @@ def main() -> int:
             "launches_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep_launches.items()},
             "persistent_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep.items()},
             "step_with_rmsnorms_us": {str(m): v for m, v in norm_steps.items()},
+            "decode_token_with_attention": {str(p): v for p, v in token_steps.items()},
             "per_projection_m1": per_kernel,
             "lm_head_argmax": {str(m): v for m, v in head.items()},
             "prefill": {str(m): v for m, v in prefill.items()},

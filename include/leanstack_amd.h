@@ -148,6 +148,39 @@ int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K,
                             int epilogue, const void* residual, int ldr,
                             void* hip_stream);
 
+/* Device workspace of lsk_decode_attention_bf16 for n_kv kv heads of
+ * n_q / n_kv q heads and caches of max_seq_len rows (0 if the geometry is not
+ * supported).  Needed once more than 512 rows are attended. */
+size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_seq_len);
+
+/* One decode token of one layer, between its QKV and o_proj projections:
+ *   q heads and k heads of `qkv` (the raw QKV projection row [n_q*d | n_kv*d |
+ *   n_kv*d], bf16) get the per-head RMSNorm over d with q_norm_weight /
+ *   k_norm_weight and eps, then rotate-half RoPE with `cos` / `sin` (bf16
+ *   [d/2], this position's row of the position cache), with a bf16 rounding
+ *   after each step as the reference's torch ops round;
+ *   k and v are written to row `pos` of k_cache / v_cache (this layer's
+ *   [n_kv][max_seq_len][d] bf16, 16-byte aligned);
+ *   out[n_q*d] = softmax(q K^T * scale) V over rows 0..pos, q head h reading
+ *   kv head h / (n_q/n_kv), fp32 scores and softmax, bf16 output.
+ * d must be 128, n_kv at most 64, n_q/n_kv one of 1, 2, 4, 8, and
+ * max_seq_len at most 16384.  The rows are split into chunks of 512, one
+ * workgroup each; with more than one chunk the partial results meet in
+ * `workspace` (lsk_attention_workspace_bytes(), 256-byte aligned,
+ * zero-filled before its first use; calls leave it zeroed; calls sharing one
+ * must be stream-ordered), combined in chunk order so results are bitwise
+ * reproducible.  With up to 512 rows the workspace may be NULL.  The caller
+ * advances its sequence length.  Replaces the per-head norms and RoPE of
+ * src/leanstack/runtime/qwen_explicit.py:796-806 (RoPE :690-716), the cache
+ * append of src/leanstack/runtime/kv_cache.py:222-245 and the
+ * F.scaled_dot_product_attention of qwen_explicit.py:894-912. */
+int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim,
+                              const void* q_norm_weight, const void* k_norm_weight, float eps,
+                              const void* cos, const void* sin,
+                              void* k_cache, void* v_cache, int max_seq_len, int pos,
+                              float scale, void* out,
+                              void* workspace, size_t ws_bytes, void* hip_stream);
+
 /* Greedy lm_head: out_idx[m] = argmax_v sum_k f32(W[v][k]) * f32(x[m][k]) for
  * m < M (M = 1..16), lowest index on ties.
  *   logits_mode  LSK_LOGITS_FP32 compares fp32 scores, as the cuTile kernel

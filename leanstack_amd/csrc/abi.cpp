@@ -228,6 +228,52 @@ int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K, c
   return LSK_OK;
 }
 
+size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_seq_len) {
+  if (head_dim != lsk::kAttnHeadDim || n_kv < 1 || n_kv > lsk::kAttnMaxKvHeads || n_q < n_kv || n_q % n_kv != 0 ||
+      !lsk::attention_group_supported(n_q / n_kv) || max_seq_len < 1 ||
+      max_seq_len > lsk::kAttnMaxChunks * lsk::kAttnChunkRows)
+    return 0;
+  return lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
+}
+
+int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim, const void* q_norm_weight,
+                              const void* k_norm_weight, float eps, const void* cos, const void* sin, void* k_cache,
+                              void* v_cache, int max_seq_len, int pos, float scale, void* out, void* workspace,
+                              size_t ws_bytes, void* hip_stream) {
+  g_last_error.clear();
+  if (head_dim != lsk::kAttnHeadDim)
+    return fail(LSK_ERR_INVALID, "head_dim=%d: the attention kernel is built for %d", head_dim, lsk::kAttnHeadDim);
+  if (n_kv < 1 || n_kv > lsk::kAttnMaxKvHeads || n_q < n_kv || n_q % n_kv != 0 ||
+      !lsk::attention_group_supported(n_q / n_kv))
+    return fail(LSK_ERR_INVALID, "n_q=%d, n_kv=%d: n_kv must be 1..%d and n_q 1, 2, 4 or 8 times n_kv", n_q, n_kv,
+                lsk::kAttnMaxKvHeads);
+  if (qkv == nullptr || q_norm_weight == nullptr || k_norm_weight == nullptr || cos == nullptr || sin == nullptr ||
+      k_cache == nullptr || v_cache == nullptr || out == nullptr)
+    return fail(LSK_ERR_INVALID, "null device pointer");
+  if (!aligned(qkv, 2) || !aligned(q_norm_weight, 2) || !aligned(k_norm_weight, 2) || !aligned(cos, 2) ||
+      !aligned(sin, 2) || !aligned(out, 2))
+    return fail(LSK_ERR_INVALID, "bf16 arguments must be 2-byte aligned");
+  if (!aligned(k_cache, 16) || !aligned(v_cache, 16))
+    return fail(LSK_ERR_INVALID, "the key and value caches must be 16-byte aligned");
+  const int max_rows = lsk::kAttnMaxChunks * lsk::kAttnChunkRows;
+  if (max_seq_len < 1 || max_seq_len > max_rows || pos < 0 || pos >= max_seq_len)
+    return fail(LSK_ERR_INVALID, "pos=%d, max_seq_len=%d: need 0 <= pos < max_seq_len <= %d", pos, max_seq_len,
+                max_rows);
+  if (!std::isfinite(eps) || eps < 0.f) return fail(LSK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
+  if (!std::isfinite(scale)) return fail(LSK_ERR_INVALID, "scale must be finite");
+  if (pos + 1 > lsk::kAttnChunkRows) {
+    const size_t need = lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
+    if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 256))
+      return fail(LSK_ERR_WORKSPACE, "attending %d rows needs a workspace of %zu bytes, 256-byte aligned (got %zu)",
+                  pos + 1, need, workspace ? ws_bytes : 0);
+  }
+  hipError_t err = lsk::launch_decode_attention(qkv, n_q, n_kv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
+                                                v_cache, max_seq_len, pos, scale, out, workspace, ws_bytes,
+                                                static_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess) return hip_fail(err, "decode attention kernel launch");
+  return LSK_OK;
+}
+
 int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
                             float* logits_opt, int logits_mode, long long* out_idx, void* workspace,
                             size_t ws_bytes, void* hip_stream) {

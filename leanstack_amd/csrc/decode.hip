@@ -152,6 +152,13 @@ __device__ __forceinline__ float sum_squares(bf16x8_t v) {
   return s;
 }
 
+// 1 / sqrt(ss / n + eps) with the mean rounded before eps is added, as
+// torch's rms_norm computes it (contraction would fuse the two into an fma).
+__device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
+#pragma clang fp contract(off)
+  return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+}
+
 // Lanes 0..15 hold this wave's partial sum of squares of rows 0..15; returns
 // r[lane % 16] for active rows and 0 for padding columns, summing the waves'
 // partials in wave order.  Every wave must call it.
@@ -163,7 +170,7 @@ __device__ __forceinline__ float row_inv_rms(float ss, int wave, int lane, int K
   float total = 0.f;
 #pragma unroll
   for (int w = 0; w < NW; ++w) total += part[w][lane & 15];
-  return m_active ? 1.0f / sqrtf(total / static_cast<float>(K) + eps) : 0.f;
+  return m_active ? inv_rms(total, K, eps) : 0.f;
 }
 
 // bf16((x * nw) * r) of one fragment; `keep` clears padding columns.  The

@@ -207,6 +207,77 @@ def _semantic_decode_attention_output_vector(query_states, key_states, value_sta
     return kernels.linear(attn.reshape(1, -1), o_w).view(-1)
 
 
+# ------------------------------------------------------------ decode layer
+
+
+def _static_cache_layer(kv_cache, layer_idx: int):
+    """The layer's [n_kv, max_seq_len, d] key / value caches and its cached
+    row count, from a static cache with the reference's interface
+    (src/leanstack/runtime/kv_cache.py:207-266: key_cache / value_cache
+    [L, B, n_kv, S, d], layer_seq_lens), batch 1."""
+    if hasattr(kv_cache, "layer_tensors"):
+        k, v = kv_cache.layer_tensors(layer_idx)
+    else:
+        if kv_cache.key_cache.shape[1] != 1:
+            raise ValueError("the decode attention kernel serves batch 1")
+        k, v = kv_cache.key_cache[layer_idx, 0], kv_cache.value_cache[layer_idx, 0]
+    return k, v, int(kv_cache.layer_seq_lens[layer_idx])
+
+
+def _advance_cache(kv_cache, layer_idx: int) -> None:
+    """Count the row the kernel wrote, as StaticKVBlockManager.append does
+    after its copy (kv_cache.py:243-245)."""
+    if hasattr(kv_cache, "advance"):
+        kv_cache.advance(layer_idx, 1)
+    else:
+        kv_cache.layer_seq_lens[layer_idx] += 1
+        kv_cache.max_layer_seq_len = max(kv_cache.max_layer_seq_len, kv_cache.layer_seq_lens[layer_idx])
+
+
+def _attend_vector(attention, qkv_states, kv_cache, position_embeddings, rms_norm_eps):
+    """q/k norms, RoPE, the cache append and GQA attention of one decode token
+    in one kernel (the work of qwen_explicit.py:796-806, kv_cache.py:222-245
+    and :894-912) -> [n_q * d]."""
+    cos, sin = position_embeddings
+    k_layer, v_layer, pos = _static_cache_layer(kv_cache, attention.layer_idx)
+    out = kernels.decode_attention(
+        qkv_states, attention.q_norm_weight, attention.k_norm_weight, rms_norm_eps, cos, sin, k_layer, v_layer, pos,
+        attention.attention_scale, num_attention_heads=attention.num_attention_heads,
+        num_key_value_heads=attention.num_key_value_heads)
+    _advance_cache(kv_cache, attention.layer_idx)
+    return out
+
+
+def _semantic_qwen_attention_decode_forward(attention, hidden_states, kv_cache, position_embeddings, rms_norm_eps):
+    """QKV GEMV, the attention kernel, o_proj GEMV (qwen_explicit.py:1147-1176) -> [H].
+    `hidden_states` is the normalised hidden state, as the reference passes it."""
+    qkv_w = _require_packed(attention.qkv_proj_weight, "qkv_proj_weight")
+    o_w = _require_packed(attention.o_proj_weight, "o_proj_weight")
+    qkv = kernels.linear(hidden_states.reshape(1, -1), qkv_w)
+    attn = _attend_vector(attention, qkv, kv_cache, position_embeddings, rms_norm_eps)
+    return kernels.linear(attn.view(1, -1), o_w).view(-1)
+
+
+def semantic_qwen_decode_layer_forward(layer, hidden_states, kv_cache, position_embeddings, rms_norm_eps):
+    """One decode layer (qwen_explicit.py:1247-1272) in five kernels:
+    input_layernorm + QKV, the attention kernel, o_proj + residual,
+    post_attention_layernorm + gate_up + SiLU*up, down + residual.
+    Returns [1, 1, H]."""
+    a = layer.attention
+    qkv_w = _require_packed(a.qkv_proj_weight, "qkv_proj_weight")
+    o_w = _require_packed(a.o_proj_weight, "o_proj_weight")
+    gu_w = _require_packed(layer.mlp.gate_up_proj_weight, "gate_up_proj_weight", _lib.LAYOUT_MFMA16X32_GATEUP)
+    d_w = _require_packed(layer.mlp.down_proj_weight, "down_proj_weight")
+    _check_gate_dim(gu_w, layer.mlp.gate_proj_out_dim)
+    residual = hidden_states.reshape(1, -1)
+    qkv = kernels.rmsnorm_linear(residual, layer.input_layernorm_weight, rms_norm_eps, qkv_w)
+    attn = _attend_vector(a, qkv, kv_cache, position_embeddings, rms_norm_eps)
+    hidden = kernels.linear(attn.view(1, -1), o_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=residual)
+    act = kernels.rmsnorm_linear(hidden, layer.post_attention_layernorm_weight, rms_norm_eps, gu_w,
+                                 epilogue=_lib.EPI_SILU_MUL)
+    return kernels.linear(act, d_w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=hidden).view(1, 1, -1)
+
+
 def semantic_qwen_mlp_forward(mlp, hidden_states):
     """gate_up + SiLU*up, down (qwen_explicit.py:1201-1208); `mlp` has
     gate_up_proj_weight, gate_proj_out_dim and down_proj_weight."""

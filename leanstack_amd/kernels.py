@@ -156,6 +156,74 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weigh
     return out
 
 
+_attention_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def attention_workspace(device: torch.device, n_q: int, n_kv: int, head_dim: int,
+                        max_seq_len: int) -> torch.Tensor:
+    """The decode attention workspace for the current stream of `device`
+    (zero-filled once, left zero-filled by every call), large enough for
+    this geometry.  One per (device, stream): calls sharing one must be
+    stream-ordered."""
+    nbytes = _lib.load().lsk_attention_workspace_bytes(n_q, n_kv, head_dim, max_seq_len)
+    if nbytes == 0:
+        raise ValueError(f"no attention workspace for n_q={n_q}, n_kv={n_kv}, head_dim={head_dim}, "
+                         f"max_seq_len={max_seq_len}")
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle() or 0)
+    ws = _attention_workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+        _attention_workspaces[key] = ws
+    return ws
+
+
+def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
+                     cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int,
+                     scale: float, *, num_attention_heads: int, num_key_value_heads: int,
+                     out: torch.Tensor | None = None, workspace: torch.Tensor | str = "auto") -> torch.Tensor:
+    """One decode token of one layer between QKV and o_proj: per-head q/k
+    RMSNorm and RoPE of the raw QKV row, k and v written to row `pos` of the
+    layer's caches ([n_kv, max_seq_len, d] bf16, batch 1), and GQA attention
+    over rows 0..pos.  Returns out [n_q * d] bf16.  The caller advances its
+    cache cursor.  workspace: "auto" (attention_workspace), or a zero-filled
+    uint8 device tensor of lsk_attention_workspace_bytes() bytes."""
+    lib = _lib.load()
+    n_q, n_kv = num_attention_heads, num_key_value_heads
+    for t, what in ((qkv, "qkv"), (q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"), (cos, "cos"),
+                    (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _require_device(t, what)
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{what} must be bfloat16, got {t.dtype}")
+    if k_cache.dim() != 3 or k_cache.shape != v_cache.shape or k_cache.shape[0] != n_kv:
+        raise ValueError(f"k_cache / v_cache must be [n_kv={n_kv}, max_seq_len, head_dim], got "
+                         f"{tuple(k_cache.shape)} / {tuple(v_cache.shape)}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache / v_cache must be contiguous")
+    d = k_cache.shape[2]
+    if qkv.numel() != (n_q + 2 * n_kv) * d:
+        raise ValueError(f"qkv has {qkv.numel()} values, expected {(n_q + 2 * n_kv) * d}")
+    if q_norm_weight.numel() != d or k_norm_weight.numel() != d or cos.numel() != d // 2 or sin.numel() != d // 2:
+        raise ValueError(f"norm weights must hold {d} values and cos / sin {d // 2} (this position's row)")
+    flat = [t.reshape(-1).contiguous() for t in (qkv, q_norm_weight, k_norm_weight, cos, sin)]
+    if out is None:
+        out = torch.empty((n_q * d,), device=qkv.device, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.numel() != n_q * d or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bfloat16 tensor of {n_q * d} values")
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError(f"workspace must be 'auto' or a tensor, not {workspace!r}")
+        workspace = attention_workspace(qkv.device, n_q, n_kv, d, k_cache.shape[1])
+    _require_device(workspace, "workspace")
+    status = lib.lsk_decode_attention_bf16(
+        flat[0].data_ptr(), n_q, n_kv, d, flat[1].data_ptr(), flat[2].data_ptr(), float(eps),
+        flat[3].data_ptr(), flat[4].data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[1], int(pos),
+        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        stream_handle(),
+    )
+    _lib.check(status, "lsk_decode_attention_bf16")
+    return out
+
+
 class LmHeadWorkspace:
     """Device workspace of the two-stage argmax, sized once per (M, V, K)."""
 

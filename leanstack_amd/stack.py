@@ -137,3 +137,68 @@ class DecodeLinearStack:
             fn()
         torch.cuda.synchronize(self.device)
         return graph
+
+
+class DecodeStep:
+    """One whole decode token (M = 1) over every layer, in the reference's
+    order (semantic_qwen_decode_layer_forward, qwen_explicit.py:1247-1272,
+    then the greedy head :952-960): per layer input_layernorm + QKV, the
+    attention kernel (q/k norms, RoPE, cache append, GQA attention), o_proj
+    + residual, post_attention_layernorm + gate_up + SiLU*up, down +
+    residual; then the final RMSNorm and the lm_head argmax.  All buffers are
+    fixed, so the launch sequence can be captured as one HIP graph; the
+    position is part of what is captured.
+
+    norms: [n, 2, H] (input / post-attention), qk_norms: [n, 2, d] (q / k),
+    k_cache / v_cache: [n, n_kv, max_seq_len, d]."""
+
+    def __init__(self, layers: list[LayerProjections], norms: torch.Tensor, qk_norms: torch.Tensor,
+                 final_norm: torch.Tensor, lm_head: PackedWeight, geometry: QwenGeometry, k_cache: torch.Tensor,
+                 v_cache: torch.Tensor, device: torch.device) -> None:
+        g = geometry
+        self.layers, self.norms, self.qk_norms, self.final_norm, self.lm_head = layers, norms, qk_norms, final_norm, \
+            lm_head
+        self.g, self.k_cache, self.v_cache, self.device = g, k_cache, v_cache, device
+        self.eps = g.rms_norm_eps
+        self.scale = g.head_dim ** -0.5
+        max_seq = k_cache.shape[2]
+        inv = 1.0 / (g.rope_theta ** (torch.arange(0, g.head_dim, 2, device=device, dtype=torch.float32) / g.head_dim))
+        freqs = torch.outer(torch.arange(max_seq, device=device, dtype=torch.float32), inv)
+        # the reference's position cache (build_qwen_position_cache, qwen_explicit.py:664-676)
+        self.cos, self.sin = freqs.cos().to(torch.bfloat16), freqs.sin().to(torch.bfloat16)
+        h = g.hidden_size
+        self.hidden = torch.zeros((2, 1, h), device=device, dtype=torch.bfloat16)  # ping-pong residual stream
+        self.mid = torch.empty((1, h), device=device, dtype=torch.bfloat16)
+        self.qkv = torch.empty((1, g.qkv_dim), device=device, dtype=torch.bfloat16)
+        self.attn = torch.empty((g.q_dim,), device=device, dtype=torch.bfloat16)
+        self.act = torch.empty((1, g.intermediate_size), device=device, dtype=torch.bfloat16)
+        self.normed = torch.empty((1, h), device=device, dtype=torch.bfloat16)
+        self.head_ws = kernels.LmHeadWorkspace(1, lm_head.n, lm_head.k, device)
+        ws_bytes = _lib.load().lsk_attention_workspace_bytes(g.num_attention_heads, g.num_key_value_heads,
+                                                               g.head_dim, max_seq)
+        self.attn_ws = torch.zeros(ws_bytes, device=device, dtype=torch.uint8)  # left zeroed by every launch
+        self.token = torch.empty((1,), device=device, dtype=torch.long)
+
+    def launch(self, pos: int) -> None:
+        """Enqueue the token at position `pos` (rows 0..pos-1 of every layer's
+        cache are the context); its input is self.hidden[0], its output
+        token self.token."""
+        g = self.g
+        cos, sin = self.cos[pos], self.sin[pos]
+        for l, p in enumerate(self.layers):
+            x, y = self.hidden[l % 2], self.hidden[(l + 1) % 2]
+            kernels.rmsnorm_linear(x, self.norms[l, 0], self.eps, p.qkv, out=self.qkv)
+            kernels.decode_attention(self.qkv, self.qk_norms[l, 0], self.qk_norms[l, 1], self.eps, cos, sin,
+                                     self.k_cache[l], self.v_cache[l], pos, self.scale,
+                                     num_attention_heads=g.num_attention_heads,
+                                     num_key_value_heads=g.num_key_value_heads, out=self.attn,
+                                     workspace=self.attn_ws)
+            kernels.linear(self.attn.view(1, -1), p.o, epilogue=_lib.EPI_RESIDUAL_ADD, residual=x, out=self.mid)
+            kernels.rmsnorm_linear(self.mid, self.norms[l, 1], self.eps, p.gate_up, epilogue=_lib.EPI_SILU_MUL,
+                                   out=self.act)
+            kernels.linear(self.act, p.down, epilogue=_lib.EPI_RESIDUAL_ADD, residual=self.mid, out=y)
+        last = self.hidden[len(self.layers) % 2]
+        # the final norm stays torch (qwen_explicit.py:952-960): one norm per token
+        self.normed.copy_(torch.nn.functional.rms_norm(last, (g.hidden_size,), self.final_norm, self.eps))
+        kernels.lm_head_argmax(self.normed, self.lm_head, logits_mode=_lib.LOGITS_BF16, workspace=self.head_ws,
+                               out=self.token)

@@ -88,6 +88,45 @@ def test_rmsnorm_linear_rejects_before_launch(kwargs, code):
     assert _lib.last_error()
 
 
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(d=64), _lib.ERR_INVALID),            # head_dim other than 128
+    (dict(n_q=24), _lib.ERR_INVALID),          # 3 q heads per kv head
+    (dict(n_q=7), _lib.ERR_INVALID),           # not a multiple of n_kv
+    (dict(n_kv=0), _lib.ERR_INVALID),
+    (dict(pos=4096), _lib.ERR_INVALID),        # pos == max_seq_len
+    (dict(pos=-1), _lib.ERR_INVALID),
+    (dict(s=20000, pos=10), _lib.ERR_INVALID),   # caches longer than 16384 rows
+    (dict(n_q=128, n_kv=128), _lib.ERR_INVALID),  # more than 64 kv heads
+    (dict(pos=600, ws=0), _lib.ERR_WORKSPACE),   # more than 512 rows need the workspace
+    (dict(pos=600, nbytes=1024), _lib.ERR_WORKSPACE),
+    (dict(kc=FAKE + 8), _lib.ERR_INVALID),     # cache misaligned
+    (dict(qkv=0), _lib.ERR_INVALID),
+    (dict(eps=-1.0), _lib.ERR_INVALID),
+    (dict(scale=float("inf")), _lib.ERR_INVALID),
+])
+def test_decode_attention_rejects_before_launch(kwargs, code):
+    a = dict(qkv=FAKE, n_q=32, n_kv=8, d=128, kc=FAKE, s=4096, pos=10, eps=1e-6, scale=128 ** -0.5, ws=FAKE,
+             nbytes=1 << 30)
+    a.update(kwargs)
+    lib = _lib.load()
+    status = lib.lsk_decode_attention_bf16(a["qkv"] or None, a["n_q"], a["n_kv"], a["d"], FAKE, FAKE, a["eps"], FAKE,
+                                           FAKE, a["kc"], FAKE, a["s"], a["pos"], a["scale"], FAKE, a["ws"] or None,
+                                           a["nbytes"], None)
+    assert status == code, _lib.last_error()
+    assert _lib.last_error()
+
+
+def test_attention_workspace_bytes():
+    """Counters for 64 kv heads, then one (m, l, acc) slot of 4 * (2G + 128G)
+    bytes per (kv head, 512-row chunk)."""
+    lib = _lib.load()
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 4096) == 256 + 8 * 8 * 4 * (2 * 4 + 128 * 4)
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 100) == 256 + 8 * 1 * 4 * (2 * 4 + 128 * 4)
+    assert lib.lsk_attention_workspace_bytes(32, 8, 64, 4096) == 0      # head_dim
+    assert lib.lsk_attention_workspace_bytes(24, 8, 128, 4096) == 0     # 3 q heads per kv head
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 16385) == 0    # too many rows
+
+
 def test_lm_head_rejects_before_launch():
     lib = _lib.load()
     ok = dict(V=151936, K=2560, M=1)

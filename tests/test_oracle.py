@@ -10,6 +10,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import brute
 from oracle import projections as ref
@@ -227,3 +228,102 @@ def test_rmsnorm_matches_float64_one_rounding():
     assert exact > 0.995
     two = brute.round_bf16(brute.round_bf16(x64 * r64) * w64)
     assert np.mean(got != two) > 0.1
+
+
+# ---------------------------------------------------------------- decode attention step
+
+
+def _bf(x):
+    return torch.tensor(np.asarray(x), dtype=torch.float32).to(torch.bfloat16)
+
+
+def test_rope_closed_forms():
+    """cos = 1, sin = 0 is the identity; cos = 0, sin = 1 maps (a, b) to
+    (-b, a) exactly: a sign error, swapped halves or a missing term fails."""
+    from oracle.attention import rope
+
+    rng = np.random.default_rng(20)
+    q = _bf(rng.standard_normal((1, 4, 1, 128)))
+    k = _bf(rng.standard_normal((1, 2, 1, 128)))
+    one, zero = torch.ones(1, 1, 64, dtype=torch.bfloat16), torch.zeros(1, 1, 64, dtype=torch.bfloat16)
+    q1, k1 = rope(q, k, one, zero)
+    assert torch.equal(q1, q) and torch.equal(k1, k)
+    q2, k2 = rope(q, k, zero, one)
+    assert torch.equal(q2, torch.cat((-q[..., 64:], q[..., :64]), dim=-1))
+    assert torch.equal(k2, torch.cat((-k[..., 64:], k[..., :64]), dim=-1))
+
+
+def test_rope_matches_float64_rotation():
+    """Random angles: each output is the float64 rotation of the bf16 inputs
+    to within the reference's per-op bf16 roundings (two products and one sum)."""
+    from oracle.attention import rope
+
+    rng = np.random.default_rng(21)
+    q = _bf(rng.standard_normal((1, 3, 1, 128)) * 2)
+    ang = rng.uniform(0, 2 * np.pi, 64)
+    cos, sin = _bf(np.cos(ang)[None, None]), _bf(np.sin(ang)[None, None])
+    out, _ = rope(q, q[:, :1], cos, sin)
+    a, b = q[..., :64].double().numpy(), q[..., 64:].double().numpy()
+    c, s = cos.double().numpy()[:, None], sin.double().numpy()[:, None]
+    exact = np.concatenate((a * c - b * s, b * c + a * s), axis=-1)
+    bound = 2.0 ** -8 * (np.abs(np.concatenate((a * c, b * c), -1)) + np.abs(np.concatenate((b * s, a * s), -1))) \
+        + 2.0 ** -8 * np.abs(exact)
+    assert np.all(np.abs(out.double().numpy() - exact) <= bound + 1e-30)
+
+
+def test_sdpa_gqa_pins():
+    """softmax(q K^T * scale) V with kv head h // G: against a float64 brute
+    force, against torch's own scaled_dot_product_attention (fp32, enable_gqa),
+    uniform keys give the mean of V, and a planted dominant key returns its row."""
+    from oracle.attention import sdpa_gqa
+
+    rng = np.random.default_rng(22)
+    n_q, n_kv, S, d = 8, 2, 37, 128
+    q = _bf(rng.standard_normal((1, n_q, 1, d)))
+    k = _bf(rng.standard_normal((1, n_kv, S, d)))
+    v = _bf(rng.standard_normal((1, n_kv, S, d)))
+    scale = d ** -0.5
+    out = sdpa_gqa(q, k, v, scale, n_q // n_kv).double().numpy()
+    q64, k64, v64 = q.double().numpy(), k.double().numpy(), v.double().numpy()
+    for h in range(n_q):
+        j = h // (n_q // n_kv)
+        s = (k64[0, j] @ q64[0, h, 0]) * scale
+        p = np.exp(s - s.max())
+        ref = (p / p.sum()) @ v64[0, j]
+        assert np.allclose(out[0, h, 0], ref, rtol=1e-2, atol=1e-2)
+    torch_out = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), scale=scale, enable_gqa=True)
+    assert torch.allclose(sdpa_gqa(q, k, v, scale, n_q // n_kv).float(), torch_out, rtol=1e-2, atol=1e-2)
+    # uniform keys -> mean of V
+    ku = k.clone()
+    ku[:] = k[:, :, :1]
+    mean = v.float().mean(dim=2, keepdim=True).repeat_interleave(n_q // n_kv, dim=1)
+    assert torch.allclose(sdpa_gqa(q, ku, v, scale, n_q // n_kv).float(), mean, rtol=0, atol=2e-2)
+    # a key aligned with q head 0 at 30x the scale dominates: head 0 returns that V row
+    kd = k.clone()
+    kd[0, 0, 5] = (q[0, 0, 0].float() * 30).to(torch.bfloat16)
+    got = sdpa_gqa(q, kd, v, scale, n_q // n_kv)
+    assert torch.allclose(got[0, 0, 0].float(), v[0, 0, 5].float(), atol=1e-2)
+
+
+
+def test_decode_attention_appends_one_row():
+    """The oracle writes exactly row `pos` of each cache (k rotated, v as is)
+    and attends over rows 0..pos only: changing a row past pos changes nothing."""
+    from oracle.attention import decode_attention, qk_heads_vector
+
+    rng = np.random.default_rng(23)
+    n_q, n_kv, d, S, pos = 4, 2, 128, 32, 9
+    qkv = _bf(rng.standard_normal((n_q + 2 * n_kv) * d))
+    qn, kn = _bf(1 + 0.1 * rng.standard_normal(d)), _bf(1 + 0.1 * rng.standard_normal(d))
+    ang = rng.uniform(0, 6, 64)
+    cos, sin = _bf(np.cos(ang)), _bf(np.sin(ang))
+    kc, vc = _bf(rng.standard_normal((n_kv, S, d))), _bf(rng.standard_normal((n_kv, S, d)))
+    out, kc2, vc2 = decode_attention(qkv, n_q, n_kv, d, qn, kn, 1e-6, cos, sin, kc, vc, pos, d ** -0.5)
+    _, k, v = qk_heads_vector(qkv, n_q, n_kv, d, qn, kn, 1e-6, cos, sin)
+    rows = [t for t in range(S) if t != pos]
+    assert torch.equal(kc2[:, rows], kc[:, rows]) and torch.equal(vc2[:, rows], vc[:, rows])
+    assert torch.equal(kc2[:, pos], k.view(n_kv, d)) and torch.equal(vc2[:, pos], v.view(n_kv, d))
+    kc_far = kc.clone()
+    kc_far[:, pos + 1:] = 100.0
+    out_far, _, _ = decode_attention(qkv, n_q, n_kv, d, qn, kn, 1e-6, cos, sin, kc_far, vc, pos, d ** -0.5)
+    assert torch.equal(out, out_far)
