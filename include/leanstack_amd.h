@@ -150,7 +150,7 @@ int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K,
 
 /* Device workspace of lsk_decode_attention_bf16 for n_kv kv heads of
  * n_q / n_kv q heads and caches of max_seq_len rows (0 if the geometry is not
- * supported).  Needed once more than 512 rows are attended. */
+ * supported).  Needed once more than 128 rows are attended. */
 size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_seq_len);
 
 /* One decode token of one layer, between its QKV and o_proj projections:
@@ -164,12 +164,13 @@ size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_se
  *   out[n_q*d] = softmax(q K^T * scale) V over rows 0..pos, q head h reading
  *   kv head h / (n_q/n_kv), fp32 scores and softmax, bf16 output.
  * d must be 128, n_kv at most 64, n_q/n_kv one of 1, 2, 4, 8, and
- * max_seq_len at most 16384.  The rows are split into chunks of 512, one
+ * max_seq_len at most 16384.  The pos+1 rows are split into at most 32
+ * chunks of 128, 256, 384 or 512 rows (the smallest that fits), one
  * workgroup each; with more than one chunk the partial results meet in
  * `workspace` (lsk_attention_workspace_bytes(), 256-byte aligned,
  * zero-filled before its first use; calls leave it zeroed; calls sharing one
  * must be stream-ordered), combined in chunk order so results are bitwise
- * reproducible.  With up to 512 rows the workspace may be NULL.  The caller
+ * reproducible.  With up to 128 rows the workspace may be NULL.  The caller
  * advances its sequence length.  Replaces the per-head norms and RoPE of
  * src/leanstack/runtime/qwen_explicit.py:796-806 (RoPE :690-716), the cache
  * append of src/leanstack/runtime/kv_cache.py:222-245 and the

@@ -231,7 +231,7 @@ int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K, c
 size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_seq_len) {
   if (head_dim != lsk::kAttnHeadDim || n_kv < 1 || n_kv > lsk::kAttnMaxKvHeads || n_q < n_kv || n_q % n_kv != 0 ||
       !lsk::attention_group_supported(n_q / n_kv) || max_seq_len < 1 ||
-      max_seq_len > lsk::kAttnMaxChunks * lsk::kAttnChunkRows)
+      max_seq_len > lsk::kAttnMaxRows)
     return 0;
   return lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
 }
@@ -255,13 +255,13 @@ int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim, 
     return fail(LSK_ERR_INVALID, "bf16 arguments must be 2-byte aligned");
   if (!aligned(k_cache, 16) || !aligned(v_cache, 16))
     return fail(LSK_ERR_INVALID, "the key and value caches must be 16-byte aligned");
-  const int max_rows = lsk::kAttnMaxChunks * lsk::kAttnChunkRows;
+  const int max_rows = lsk::kAttnMaxRows;
   if (max_seq_len < 1 || max_seq_len > max_rows || pos < 0 || pos >= max_seq_len)
     return fail(LSK_ERR_INVALID, "pos=%d, max_seq_len=%d: need 0 <= pos < max_seq_len <= %d", pos, max_seq_len,
                 max_rows);
   if (!std::isfinite(eps) || eps < 0.f) return fail(LSK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
   if (!std::isfinite(scale)) return fail(LSK_ERR_INVALID, "scale must be finite");
-  if (pos + 1 > lsk::kAttnChunkRows) {
+  if (pos + 1 > lsk::kAttnMinChunkRows) {
     const size_t need = lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
     if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 256))
       return fail(LSK_ERR_WORKSPACE, "attending %d rows needs a workspace of %zu bytes, 256-byte aligned (got %zu)",

@@ -58,18 +58,36 @@ __device__ __forceinline__ __bf16 rope_half(float a, float b, float c, float s, 
   return static_cast<__bf16>(bf16r(a * c) + sign * bf16r(b * s));
 }
 
-// Butterfly sum / max: partners add the same two values, so every lane ends
-// with the identical result.
+// Wave-wide sum / max with the butterfly's pairing (xor 1, 2, 4, 8 inside a
+// 16-lane row, then (r0 + r1) + (r2 + r3) over the rows).  The in-row steps
+// are DPP moves (quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and
+// row_mirror: after the quad steps every lane of a quad holds the quad's
+// value, so mirroring pairs each quad / half with the other one); partners
+// combine the same two values, so every lane of a row holds identical bits.
+// The rows are combined from readlanes, so all lanes get one value.
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row_lane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  v += dpp<0xb1>(v);
+  v += dpp<0x4e>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-  return v;
+  v = fmaxf(v, dpp<0xb1>(v));
+  v = fmaxf(v, dpp<0x4e>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
 }
 
 struct AttnArgs {
@@ -84,7 +102,7 @@ struct AttnArgs {
   unsigned* counters;      // workspace: one arrival counter per kv head
   unsigned char* partials; // workspace: one AttnPartial slot per (kv head, chunk)
   unsigned partial_bytes;  // bytes of all slots of this launch
-  int n_q, n_kv, s_max, pos, chunks;
+  int n_q, n_kv, s_max, pos, chunks;  // chunks of 128 * NU rows
   float eps, scale;
 };
 
@@ -98,11 +116,68 @@ __host__ __device__ constexpr unsigned partial_slot_bytes(int G) {
   return (unsigned)(G * 2 + G * kAttnHeadDim) * 4u + 12u & ~15u;
 }
 
-template <int G>
+// The last workgroup of kv head j: M_h = max_c m_c and
+// out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c, in chunk order.
+// Every partial value is requested in one round (NB * 8 chunk slots per
+// output, those past the last chunk re-read the last one and get weight 0),
+// together with the (m, l) pairs, so the combine waits for memory once.
+template <int G, int NB>
+__device__ __forceinline__ void combine_chunks(const AttnArgs& a, __amdgpu_buffer_rsrc_t parts, unsigned first,
+                                               unsigned slot_bytes, int j, float (*mx)[G], float (*lsum)[G],
+                                               float (*wts)[G], float (*wl)[G]) {
+  constexpr int kOut = (G * kHeadDim + kThreads - 1) / kThreads;
+  constexpr int kSlots = NB * 8;
+  float v[kOut][kSlots];
+#pragma unroll
+  for (int o = 0; o < kOut; ++o) {
+    const int e = min((int)threadIdx.x + o * kThreads, G * kHeadDim - 1);
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) {
+      const unsigned kc = (unsigned)min(k, a.chunks - 1);
+      v[o][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, (unsigned)(2 * G + e) * 4u,
+                                                                              first + kc * slot_bytes, kCoherent));
+    }
+  }
+  // (m, l) of chunk k, head h, to thread kG + h; weights past the last
+  // chunk are 0.
+  const int wk = threadIdx.x / G;
+  const int wh = threadIdx.x - wk * G;
+  if (wk < a.chunks) {
+    const unsigned base = first + wk * slot_bytes;
+    mx[wk][wh] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, (unsigned)wh * 4u, base,
+                                                                                  kCoherent));
+    lsum[wk][wh] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, (unsigned)(G + wh) * 4u,
+                                                                                    base, kCoherent));
+  }
+  __syncthreads();
+  if (wk < kSlots) {
+    float m = -__builtin_huge_valf();
+    for (int k = 0; k < a.chunks; ++k) m = fmaxf(m, mx[k][wh]);
+    const float w = wk < a.chunks ? expf(mx[wk][wh] - m) : 0.f;
+    wts[wk][wh] = w;
+    wl[wk][wh] = wk < a.chunks ? w * lsum[wk][wh] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int o = 0; o < kOut; ++o) {
+    const int e = threadIdx.x + o * kThreads;
+    if (e >= G * kHeadDim) break;
+    const int h = e / kHeadDim;
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) {
+      num += wts[k][h] * v[o][k];
+      den += wl[k][h];
+    }
+    a.out[(size_t)(j * G) * kHeadDim + e] = static_cast<__bf16>(num / den);
+  }
+}
+
+template <int G, int NU>
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) {
   static_assert(G >= 1 && G <= 16, "q heads per kv head are the MFMA B columns");
-  constexpr int kRows = kAttnChunkRows;  // rows per workgroup
-  constexpr int kGroups = kRows / 16 / kWaves;  // 16-row groups per wave: 4
+  constexpr int kGroups = NU;              // 16-row groups per wave
+  constexpr int kRows = 16 * kWaves * NU;  // rows per workgroup: 128 NU
   constexpr int kMaxChunks = kAttnMaxChunks;
   const int j = blockIdx.x / a.chunks;
   const int ci = blockIdx.x - j * a.chunks;
@@ -112,8 +187,8 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   const int c = lane & 15;
   const int L = a.pos + 1;
   const int row0 = ci * kRows;
-  // Wave w owns the chunk's 16-row groups w, w + 8, w + 16, w + 24: group u
-  // of the wave starts at chunk row lb(u) = 16 (w + 8u).  Groups past the last
+  // Wave w owns the chunk's 16-row groups w, w + 8, w + 16, ...: group u of
+  // the wave starts at chunk row lb(u) = 16 (w + 8u).  Groups past the last
   // row are skipped, so short contexts cost little and the waves share the
   // rows evenly.
   auto lb = [&](int u) { return 16 * (wave + kWaves * u); };
@@ -124,9 +199,10 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   __shared__ __align__(16) float sc[G][kRows];          // scores, then exp(s - m)
   __shared__ __align__(16) float part[kWaves][G][kHeadDim];
   __shared__ float stat[2][G];                          // chunk max, chunk sum
-  __shared__ float wts[kMaxChunks][G];                  // combine: chunk maxima, then e^(m_c - M)
-  __shared__ float lsum[kMaxChunks][G];                 // combine: chunk sums
-  __shared__ float denom[G];
+  __shared__ float cmax[kMaxChunks][G];                 // combine: chunk maxima m_c
+  __shared__ float lsum[kMaxChunks][G];                 // combine: chunk sums l_c
+  __shared__ float wts[kMaxChunks][G];                  // combine: e^(m_c - M)
+  __shared__ float wl[kMaxChunks][G];                   // combine: e^(m_c - M) l_c
   __shared__ int last;
 
   // ---- inputs of this wave's prologue items, loaded before the cache rows
@@ -246,22 +322,25 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   }
   __syncthreads();
 
-  // ---- chunk softmax state per head over its rows (kRows / 64 per lane,
-  // summed in row order within a lane, then across lanes); rows past the
-  // last get weight 0 (their score slots were never written).
+  // ---- chunk softmax state per head over its filled rows n (up to
+  // kRows / 64 per lane, summed in row order within a lane, then across
+  // lanes); the rows past the last are never read again.
+  const int n = min(kRows, L - row0);
   for (int h = wave; h < G; h += kWaves) {
     float sv[kRows / 64];
     float mx = -__builtin_huge_valf();
 #pragma unroll
     for (int u = 0; u < kRows / 64; ++u) {
-      sv[u] = row0 + lane + 64 * u < L ? sc[h][lane + 64 * u] : -__builtin_huge_valf();
+      if (64 * u >= n) break;
+      sv[u] = lane + 64 * u < n ? sc[h][lane + 64 * u] : -__builtin_huge_valf();
       mx = fmaxf(mx, sv[u]);
     }
     const float m = wave_max(mx);
     float sum = 0.f;
 #pragma unroll
     for (int u = 0; u < kRows / 64; ++u) {
-      const float e = row0 + lane + 64 * u < L ? expf(sv[u] - m) : 0.f;
+      if (64 * u >= n) break;
+      const float e = lane + 64 * u < n ? expf(sv[u] - m) : 0.f;
       sc[h][lane + 64 * u] = e;
       sum += e;
     }
@@ -274,7 +353,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   __syncthreads();
 
   // ---- P.V over this wave's groups: lane (g, c) sums rows lb(u) + 4i + g
-  // for dims 8c .. 8c+7, then the four row phases g are added (butterfly)
+  // for dims 8c .. 8c+7, then the four row phases g are added as
+  // (g0 + g1) + (g2 + g3) by a reduce-scatter (each exchange sends half of
+  // what a lane holds, so lane (g, c) ends with a quarter of the 8G sums),
   // and the waves' sums in wave order.
   float acc8[G][8];
 #pragma unroll
@@ -295,22 +376,24 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
       }
     }
   }
+  constexpr int kHalf = 4 * G;  // of the 8G values (flat index q = 8h + e)
+  const bool odd = g & 1, high = g >> 1;
+  float half[kHalf];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = acc8[h][e];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      acc8[h][e] = v;
-    }
+  for (int q = 0; q < kHalf; ++q) {
+    const float lo = acc8[q / 8][q % 8], hi = acc8[(q + kHalf) / 8][(q + kHalf) % 8];
+    half[q] = (odd ? hi : lo) + __shfl_xor(odd ? lo : hi, 16);
   }
-  if (g == 0) {
+  // lane (g, c) now holds flat indices kHalf * odd + q, q < kHalf
+  float quarter[kHalf / 2];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part[wave][h][8 * c + e] = acc8[h][e];
+  for (int q = 0; q < kHalf / 2; ++q) {
+    const float lo = half[q], hi = half[q + kHalf / 2];
+    quarter[q] = (high ? hi : lo) + __shfl_xor(high ? lo : hi, 32);
   }
+  const int q0 = kHalf * odd + (kHalf / 2) * high;
+#pragma unroll
+  for (int q = 0; q < kHalf / 2; ++q) part[wave][(q0 + q) / 8][8 * c + (q0 + q) % 8] = quarter[q];
   __syncthreads();
 
   if (a.chunks == 1) {
@@ -355,64 +438,52 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   __syncthreads();
   if (!last) return;
 
-  // Combine: M_h = max_c m_c, out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
-  // All (m, l) pairs come in one round of loads; the partial values in
-  // rounds of 8 chunks (loads past the last chunk are skipped).
   const unsigned first = (unsigned)(j * a.chunks) * slot_bytes;
-  for (int e = threadIdx.x; e < a.chunks * G; e += kThreads) {
-    const int k = e / G;
-    const int h = e - k * G;
-    const unsigned base = first + k * slot_bytes;
-    wts[k][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, (unsigned)h * 4u, base,
-                                                                                 kCoherent));
-    lsum[k][h] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, (unsigned)(G + h) * 4u, base,
-                                                                                  kCoherent));
-  }
-  __syncthreads();
-  if (threadIdx.x < G) {
-    const int h = threadIdx.x;
-    float mx = -__builtin_huge_valf();
-    for (int k = 0; k < a.chunks; ++k) mx = fmaxf(mx, wts[k][h]);
-    float den = 0.f;
-    for (int k = 0; k < a.chunks; ++k) {
-      const float w = expf(wts[k][h] - mx);
-      wts[k][h] = w;
-      den += w * lsum[k][h];
-    }
-    denom[h] = den;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < G * kHeadDim; e += kThreads) {
-    const int h = e / kHeadDim;
-    float num = 0.f;
-    for (int k = 0; k < a.chunks; k += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        v[u] = k + u < a.chunks ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                                parts, (unsigned)(2 * G + e) * 4u,
-                                                                first + (k + u) * slot_bytes, kCoherent))
-                                : 0.f;
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (k + u < a.chunks) num += wts[k + u][h] * v[u];
-    }
-    a.out[(size_t)(j * G) * kHeadDim + e] = static_cast<__bf16>(num / denom[h]);
+  if (a.chunks <= 8) {
+    combine_chunks<G, 1>(a, parts, first, slot_bytes, j, cmax, lsum, wts, wl);
+  } else if (a.chunks <= 16) {
+    combine_chunks<G, 2>(a, parts, first, slot_bytes, j, cmax, lsum, wts, wl);
+  } else if (a.chunks <= 24) {
+    combine_chunks<G, 3>(a, parts, first, slot_bytes, j, cmax, lsum, wts, wl);
+  } else {
+    combine_chunks<G, 4>(a, parts, first, slot_bytes, j, cmax, lsum, wts, wl);
   }
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G>
-hipError_t launch_g(const AttnArgs& a, hipStream_t stream) {
-  decode_attention_kernel<G><<<dim3(a.n_kv * a.chunks), dim3(kThreads), 0, stream>>>(a);
+template <int G, int NU>
+hipError_t launch_gu(const AttnArgs& a, hipStream_t stream) {
+  decode_attention_kernel<G, NU><<<dim3(a.n_kv * a.chunks), dim3(kThreads), 0, stream>>>(a);
   return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_g(const AttnArgs& a, int nu, hipStream_t stream) {
+  switch (nu) {
+    case 1:
+      return launch_gu<G, 1>(a, stream);
+    case 2:
+      return launch_gu<G, 2>(a, stream);
+    case 3:
+      return launch_gu<G, 3>(a, stream);
+    case 4:
+      return launch_gu<G, 4>(a, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
 
+int attention_chunk_rows(int rows) {
+  const int units = (rows + kAttnMinChunkRows - 1) / kAttnMinChunkRows;  // 128-row units
+  return kAttnMinChunkRows * ((units + kAttnMaxChunks - 1) / kAttnMaxChunks);
+}
+
 size_t attention_workspace_bytes(int n_q, int n_kv, int max_seq_len) {
   const int group = n_q / n_kv;
-  const size_t chunks = ((size_t)max_seq_len + kAttnChunkRows - 1) / kAttnChunkRows;
+  const int most = (max_seq_len + kAttnMinChunkRows - 1) / kAttnMinChunkRows;
+  const size_t chunks = most < kAttnMaxChunks ? most : kAttnMaxChunks;
   return kAttnPartialsOffset + (size_t)n_kv * chunks * partial_slot_bytes(group);
 }
 
@@ -435,7 +506,9 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
   a.n_kv = n_kv;
   a.s_max = s_max;
   a.pos = pos;
-  a.chunks = (pos + 1 + kAttnChunkRows - 1) / kAttnChunkRows;
+  const int rows = attention_chunk_rows(pos + 1);
+  const int nu = rows / kAttnMinChunkRows;
+  a.chunks = (pos + 1 + rows - 1) / rows;
   a.eps = eps;
   a.scale = scale;
   auto* ws = static_cast<unsigned char*>(workspace);
@@ -445,13 +518,13 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
   a.partial_bytes = (unsigned)(pb < 0x7fffffffu ? pb : 0x7fffffffu);
   switch (n_q / n_kv) {
     case 1:
-      return launch_g<1>(a, stream);
+      return launch_g<1>(a, nu, stream);
     case 2:
-      return launch_g<2>(a, stream);
+      return launch_g<2>(a, nu, stream);
     case 4:
-      return launch_g<4>(a, stream);
+      return launch_g<4>(a, nu, stream);
     case 8:
-      return launch_g<8>(a, stream);
+      return launch_g<8>(a, nu, stream);
     default:
       return hipErrorInvalidValue;
   }

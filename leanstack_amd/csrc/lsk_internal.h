@@ -99,22 +99,29 @@ hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void*
                                         const void* norm_w, float eps, void* y, int ldy, Epilogue epi,
                                         const void* residual, int ldr, hipStream_t stream);
 
-// Decode attention (attention.hip).  Rows of the cache are split into chunks
-// of kAttnChunkRows, one workgroup per (kv head, chunk).  Workspace: one
-// arrival counter per kv head (kAttnMaxKvHeads words), then from
-// kAttnPartialsOffset one partial slot per (kv head, chunk).  Zero-filled
-// before first use; every launch leaves the counters zero.
+// Decode attention (attention.hip).  The rows attended are split into at
+// most kAttnMaxChunks chunks of the smallest multiple of kAttnMinChunkRows
+// that allows it (attention_chunk_rows), one workgroup per (kv head, chunk).
+// Workspace: one arrival counter per kv head (kAttnMaxKvHeads words), then
+// from kAttnPartialsOffset one partial slot per (kv head, chunk).
+// Zero-filled before first use; every launch leaves the counters zero.
 constexpr int kAttnHeadDim = 128;
-constexpr int kAttnChunkRows = 512;
-constexpr int kAttnMaxChunks = 32;  // rows attended <= 16384
+constexpr int kAttnMinChunkRows = 128;
+constexpr int kAttnMaxChunkRows = 512;
+constexpr int kAttnMaxChunks = 32;
+constexpr int kAttnMaxRows = kAttnMaxChunks * kAttnMaxChunkRows;  // 16384
 constexpr int kAttnMaxKvHeads = 64;
 constexpr size_t kAttnPartialsOffset = kAttnMaxKvHeads * 4;
 
 // q heads per kv head the attention kernel is built for.
 bool attention_group_supported(int group);
 
+// Rows per chunk when `rows` rows are attended: 128, 256, 384 or 512.
+int attention_chunk_rows(int rows);
+
 // Workspace bytes for n_kv kv heads of n_q / n_kv q heads and up to
-// max_seq_len rows (needed when more than kAttnChunkRows rows are attended).
+// max_seq_len rows (needed when more than kAttnMinChunkRows rows are
+// attended).
 size_t attention_workspace_bytes(int n_q, int n_kv, int max_seq_len);
 
 // One new token of one layer: q/k norms, RoPE, KV-cache append at row `pos`,

@@ -97,7 +97,7 @@ def test_rmsnorm_linear_rejects_before_launch(kwargs, code):
     (dict(pos=-1), _lib.ERR_INVALID),
     (dict(s=20000, pos=10), _lib.ERR_INVALID),   # caches longer than 16384 rows
     (dict(n_q=128, n_kv=128), _lib.ERR_INVALID),  # more than 64 kv heads
-    (dict(pos=600, ws=0), _lib.ERR_WORKSPACE),   # more than 512 rows need the workspace
+    (dict(pos=128, ws=0), _lib.ERR_WORKSPACE),   # more than 128 rows need the workspace
     (dict(pos=600, nbytes=1024), _lib.ERR_WORKSPACE),
     (dict(kc=FAKE + 8), _lib.ERR_INVALID),     # cache misaligned
     (dict(qkv=0), _lib.ERR_INVALID),
@@ -118,10 +118,13 @@ def test_decode_attention_rejects_before_launch(kwargs, code):
 
 def test_attention_workspace_bytes():
     """Counters for 64 kv heads, then one (m, l, acc) slot of 4 * (2G + 128G)
-    bytes per (kv head, 512-row chunk)."""
+    bytes per (kv head, chunk); at most 32 chunks of at least 128 rows."""
     lib = _lib.load()
-    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 4096) == 256 + 8 * 8 * 4 * (2 * 4 + 128 * 4)
-    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 100) == 256 + 8 * 1 * 4 * (2 * 4 + 128 * 4)
+    slot = 4 * (2 * 4 + 128 * 4)
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 4096) == 256 + 8 * 32 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 16384) == 256 + 8 * 32 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 1000) == 256 + 8 * 8 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 100) == 256 + 8 * 1 * slot
     assert lib.lsk_attention_workspace_bytes(32, 8, 64, 4096) == 0      # head_dim
     assert lib.lsk_attention_workspace_bytes(24, 8, 128, 4096) == 0     # 3 q heads per kv head
     assert lib.lsk_attention_workspace_bytes(32, 8, 128, 16385) == 0    # too many rows

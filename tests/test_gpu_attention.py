@@ -65,11 +65,20 @@ def _check_case(n_q, n_kv, s_max, pos, seed):
     assert (kdiff <= k2[:, pos].float().abs() * 2.0 ** -7 + 1e-30).all(), f"{what}: k row beyond one bf16 step"
 
 
-@pytest.mark.parametrize("pos", [0, 1, 2, 15, 16, 17, 63, 64, 127, 128, 319, 511, 512, 513, 1000, 4095])
+@pytest.mark.parametrize("pos", [0, 1, 2, 15, 16, 17, 63, 64, 127, 128, 319, 511, 512, 513, 1000, 1023, 1024,
+                                 2047, 3071, 3072, 4095])
 def test_decode_attention_qwen3_4b(gpu, pos):
-    """32 q heads, 8 kv heads, head_dim 128, a 4096-row cache: one 512-row
-    chunk up to pos 511, then several chunks combined through the workspace."""
+    """32 q heads, 8 kv heads, head_dim 128, a 4096-row cache: one 128-row
+    chunk up to pos 127, then 2..32 chunks combined through the workspace
+    (8, 16, 24 and 32 chunk slots per combine round at the edges)."""
     _check_case(G.num_attention_heads, G.num_key_value_heads, 4096, pos, seed=9000 + pos)
+
+
+@pytest.mark.parametrize("pos", [4096, 8191, 8192, 12287, 12288, 16383])
+def test_decode_attention_long_cache(gpu, pos):
+    """A 16384-row cache: chunks of 256, 384 and 512 rows once more than
+    4096, 8192 and 12288 rows are attended."""
+    _check_case(G.num_attention_heads, G.num_key_value_heads, 16384, pos, seed=9300 + pos)
 
 
 @pytest.mark.parametrize("n_q", [2, 4, 16])
