@@ -610,16 +610,113 @@ hipError_t launch_decode_cfg(const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Half-block form for M <= 8: workgroup b covers rows 8h .. 8h+7 (h = b & 1)
+// of row-block(s) (b >> 1) * RBW .., so a projection has twice as many,
+// half-sized workgroups.  One wave load still moves 1 KB of whole 128-byte
+// lines: lanes with c < 8 read the 8 rows of k-tile 2p (their chunks of a
+// packed tile are lines 0, 2, 4, 6 or 1, 3, 5, 7), lanes with c >= 8 the
+// same rows of k-tile 2p + 1.  The activation fragments of tile 2p go to B
+// columns 0..M-1, those of tile 2p + 1 to columns M..2M-1, so output row
+// 8h + i (i < 8) of x row m is D[i][m] + D[8 + i][M + m] (even tiles plus
+// odd tiles, added once after the wave reduction).  Grid: 2 * NB / RBW
+// workgroups of NW waves; K/32 == 2 * NW * U (single-round loads).
+// With 16-row workgroups the QKV projection (384 row-blocks) leaves half of
+// the 256 CUs with one workgroup and half with two, and gate_up (608 pairs)
+// runs a third round on 96 CUs; halves make 3 per CU and 4.75 per CU.
+template <int NW, int RBW, int EPI, int U>
+__global__ __launch_bounds__(NW * 64) void decode_half_kernel(
+    const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, __bf16* __restrict__ y,
+    int ldy, const __bf16* __restrict__ residual, int ldr, int M, int KT) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int h = blockIdx.x & 1;
+  const int rb0 = (blockIdx.x >> 1) * RBW;
+  const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + (c >> 3) * 64 + g * 16 + 8 * h + (c & 7);
+  const bool b_lo = c < M;
+  const bool b_hi = c >= M && c < 2 * M;
+  const unsigned keep = (b_lo || b_hi) ? 0xffffffffu : 0u;
+  const int xr = b_lo ? c : (b_hi ? c - M : 0);
+  const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)xr * ldx) + (b_hi ? 4 : 0) + g;
+  f32x4_t acc[RBW];
+#pragma unroll
+  for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int pb = wave * U;
+  bf16x8_t wv[U][RBW];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + 2 * (pb + u)) * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bf16x8_t xv = load_x_frag(xrow + (pb + u) * 8, keep);
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xv, acc[r]);
+  }
+  if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
+  const int partner = lane + 32 + M;  // only read where g < 2 and c < M (partner < 64)
+#pragma unroll
+  for (int r = 0; r < RBW; ++r) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[r][i] += __shfl(acc[r][i], partner & 63);
+  }
+  if (g >= 2 || c >= M) return;
+  const int m = c;
+  if constexpr (EPI == static_cast<int>(Epilogue::kSiluMul)) {
+    const int j = (blockIdx.x >> 1) * 16 + 8 * h + 4 * g;
+    unsigned short o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = bf16_bits(silu_mul_bf16(acc[0][i], acc[1][i]));
+    *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + j) =
+        u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+  } else {
+#pragma unroll
+    for (int r = 0; r < RBW; ++r) {
+      const int n = (rb0 + r) * 16 + 8 * h + 4 * g;
+      unsigned short o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = bf16_round(acc[r][i]);
+        if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd))
+          v = bf16_to_f32(residual[(size_t)m * ldr + n + i]) + v;
+        o[i] = bf16_bits(v);
+      }
+      *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
+          u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+    }
+  }
+}
+
+template <int NW, int RBW, int EPI, int U>
+hipError_t launch_half_cfg(const DecodeArgs& a, hipStream_t stream) {
+  decode_half_kernel<NW, RBW, EPI, U><<<dim3(a.NB / RBW * 2), dim3(NW * 64), 0, stream>>>(
+      static_cast<const bf16x8_t*>(a.w), static_cast<const __bf16*>(a.x), a.ldx, static_cast<__bf16*>(a.y), a.ldy,
+      static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT);
+  return hipGetLastError();
+}
+
 // Shape dispatch: the Qwen3-4B K values get single-round instantiations
 // (K/32 = 80 -> 16 waves x 5 for QKV and the gate/up pairs, 128 -> 8 x 16,
 // 304 -> 16 x 19, each measured faster than the alternatives on MI355X); any
 // other K runs the round-based variant.
 template <int RBW, int EPI>
 hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
+  // K/32 = 80 at M <= 8 (QKV and gate_up, 36-layer step at M = 1):
+  // half-blocks, QKV 8 waves x 5 pairs, gate_up 4 waves x 10 pairs; measured
+  // 55 us (3.6 %) faster per step than 16-row workgroups.  o_proj and down
+  // (160 row-blocks) measured slower as halves: 320 workgroups leave 64 CUs
+  // with two.
+  if (a.KT == 80 && a.M <= 8) {
+    if constexpr (RBW == 1) return launch_half_cfg<8, RBW, EPI, 5>(a, stream);
+    if constexpr (RBW == 2) return launch_half_cfg<4, RBW, EPI, 10>(a, stream);
+  }
   switch (a.KT) {
     case 80:
-      // 16 waves x 5 k-tiles, for the single row-block (QKV) and the gate/up
-      // pair alike: measured 4.5 % / 3.2 % faster than 8 waves x 10 (whose
+      // (M > 8) 16 waves x 5 k-tiles, for the single row-block (QKV) and the
+      // gate/up pair alike: measured 4.5 % / 3.2 % faster than 8 waves x 10 (whose
       // gate/up form needs 96 VGPRs and leaves 96 of 608 workgroups for a
       // second wave) and than the round-based loop.
       return launch_decode_cfg<16, RBW, EPI, 5, 0>(a, stream);

@@ -113,15 +113,18 @@ def test_rmsnorm_linear_exact_sum_rows(gpu, name, m):
     of 1/16 far below 2^20, so r is the same in any summation order; and every
     x is a power of two, so x * r and x * nw are exact and the kernel's order
     (x * nw) * r rounds to the same value as the oracle's (x * r) * nw.  The
-    fused output then equals the unfused kernel on the oracle's rows bit for
-    bit."""
+    weight rows are one-hot, so each projection output is one normalised value
+    (a single-term sum, the same in any accumulation order or kernel shape):
+    the fused output then equals the unfused kernel on the oracle's rows bit
+    for bit."""
     n, k, layout, epi = CASES[name]
     gen = torch.Generator().manual_seed(8000 + m)
     mag = torch.tensor([0.25, 0.5, 1.0, 2.0])[torch.randint(0, 4, (m, k), generator=gen)]
     sign = torch.randint(0, 2, (m, k), generator=gen).float() * 2 - 1
     x = (mag * sign).to(torch.bfloat16)
     nw = _norm_weight(k, 8100 + m)
-    w = weight(n, k, seed=8200 + m)
+    w = torch.zeros((n, k), dtype=torch.bfloat16)
+    w[torch.arange(n), (torch.arange(n) * 7 + m) % k] = 1.0
     pw = PackedWeight.from_rowmajor(w.to(DEV), layout)
     y = _fused(x, nw, pw, epi)
     xn = ref.rmsnorm(x, nw, EPS)
