@@ -227,13 +227,17 @@ __host__ __device__ constexpr int rms_wave_bytes(int U, int NC, int M, int RBW) 
 // scaling run while the weights are in flight.  The normalised rows are
 // staged in this wave's LDS area and read back as B fragments.  Sums are
 // taken in a fixed order (chunks in K order within a wave, then waves in
-// order), so results are bitwise reproducible.
-template <int NW, int RBW, int U, int NC>
+// order), so results are bitwise reproducible.  HALF: the half-block form of
+// decode_half_kernel (U k-tiles = U/2 pairs; wt is the lane's half-block
+// pointer; B column c < M reads row c of tile 2p, M <= c < 2M row c - M of
+// tile 2p + 1).
+template <int NW, int RBW, int U, int NC, bool HALF = false>
 __device__ __forceinline__ void accumulate_rows_rms_dense(f32x4_t (&acc)[RBW], const bf16x8_t* __restrict__ wt,
                                                           const __bf16* __restrict__ x, int ldx,
                                                           const bf16x8_t* __restrict__ nw, int M, int KT, int kb,
                                                           int wave, int lane, float eps) {
   constexpr int kRowChunks = U * 4;     // chunks of 8 values per row of the slice
+  static_assert(kRowChunks <= 64, "one lane per norm-weight chunk of the slice");
   constexpr int kRowStride = U * 32 + 8;  // bf16 per staged row: 16 rows start on 16 distinct bank quads
   unsigned char* area = rms_lds + (size_t)wave * rms_wave_bytes(U, NC, M, RBW);
   u32x4_t* nws = reinterpret_cast<u32x4_t*>(area);
@@ -256,11 +260,13 @@ __device__ __forceinline__ void accumulate_rows_rms_dense(f32x4_t (&acc)[RBW], c
     xd[i] = *reinterpret_cast<const bf16x8_t*>(x + (size_t)mc * ldx + (kb * 4 + j) * 8);
   }
   __builtin_amdgcn_sched_barrier(0);
-  bf16x8_t wv[U][RBW];
+  constexpr int kLoads = HALF ? U / 2 : U;  // weight loads per row-block (1 KB each)
+  bf16x8_t wv[kLoads][RBW];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
+  for (int u = 0; u < kLoads; ++u) {
 #pragma unroll
-    for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kb + u) * 64);
+    for (int r = 0; r < RBW; ++r)
+      wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kb + (HALF ? 2 * u : u)) * 64);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -289,11 +295,24 @@ __device__ __forceinline__ void accumulate_rows_rms_dense(f32x4_t (&acc)[RBW], c
     // Lanes past the last chunk store the last chunk's own value again.
     *reinterpret_cast<bf16x8_t*>(xs + mc * kRowStride + j * 8) = o;
   }
+  if constexpr (HALF) {
+    // Column m: row m of the even tile, row m - M of the odd one; columns
+    // past 2M read row M-1 (finite, never stored).
+    const int hi = m >= M && m < 2 * M ? 1 : 0;
+    const int row = m < M ? m : (hi ? m - M : M - 1);
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + mr * kRowStride + u * 32 + g * 8);
+    for (int u = 0; u < kLoads; ++u) {
+      const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + row * kRowStride + (2 * u + hi) * 32 + g * 8);
 #pragma unroll
-    for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + mr * kRowStride + u * 32 + g * 8);
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+    }
   }
 }
 
@@ -623,10 +642,11 @@ hipError_t launch_decode_cfg(const DecodeArgs& a, hipStream_t stream) {
 // With 16-row workgroups the QKV projection (384 row-blocks) leaves half of
 // the 256 CUs with one workgroup and half with two, and gate_up (608 pairs)
 // runs a third round on 96 CUs; halves make 3 per CU and 4.75 per CU.
-template <int NW, int RBW, int EPI, int U>
+template <int NW, int RBW, int EPI, int U, int NORM>
 __global__ __launch_bounds__(NW * 64) void decode_half_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, __bf16* __restrict__ y,
-    int ldy, const __bf16* __restrict__ residual, int ldr, int M, int KT) {
+    int ldy, const __bf16* __restrict__ residual, int ldr, int M, int KT, const __bf16* __restrict__ norm_w,
+    float eps) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
@@ -643,20 +663,30 @@ __global__ __launch_bounds__(NW * 64) void decode_half_kernel(
 #pragma unroll
   for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const int pb = wave * U;
-  bf16x8_t wv[U][RBW];
+  if constexpr (NORM > 0) {
+    (void)xrow;
+    (void)keep;
+    accumulate_rows_rms_dense<NW, RBW, 2 * U, NORM, true>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w),
+                                                          M, KT, 2 * pb, wave, lane, eps);
+    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(2 * U, NORM, M, RBW))) return;
+  } else {
+    (void)norm_w;
+    (void)eps;
+    bf16x8_t wv[U][RBW];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
-    for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + 2 * (pb + u)) * 64);
+      for (int r = 0; r < RBW; ++r) wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + 2 * (pb + u)) * 64);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bf16x8_t xv = load_x_frag(xrow + (pb + u) * 8, keep);
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xv, acc[r]);
+    }
+    if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
   }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const bf16x8_t xv = load_x_frag(xrow + (pb + u) * 8, keep);
-#pragma unroll
-    for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xv, acc[r]);
-  }
-  if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
   const int partner = lane + 32 + M;  // only read where g < 2 and c < M (partner < 64)
 #pragma unroll
   for (int r = 0; r < RBW; ++r) {
@@ -690,11 +720,12 @@ __global__ __launch_bounds__(NW * 64) void decode_half_kernel(
   }
 }
 
-template <int NW, int RBW, int EPI, int U>
+template <int NW, int RBW, int EPI, int U, int NORM = 0>
 hipError_t launch_half_cfg(const DecodeArgs& a, hipStream_t stream) {
-  decode_half_kernel<NW, RBW, EPI, U><<<dim3(a.NB / RBW * 2), dim3(NW * 64), 0, stream>>>(
+  const size_t lds = NORM > 0 ? (size_t)NW * rms_wave_bytes(2 * U, NORM, a.M, RBW) : 0;
+  decode_half_kernel<NW, RBW, EPI, U, NORM><<<dim3(a.NB / RBW * 2), dim3(NW * 64), lds, stream>>>(
       static_cast<const bf16x8_t*>(a.w), static_cast<const __bf16*>(a.x), a.ldx, static_cast<__bf16*>(a.y), a.ldy,
-      static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT);
+      static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT, static_cast<const __bf16*>(a.norm_w), a.eps);
   return hipGetLastError();
 }
 
@@ -739,6 +770,12 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
 // the round-based prologue.
 template <int RBW, int EPI>
 hipError_t launch_rms_shape(const DecodeArgs& a, hipStream_t stream) {
+  // Half-blocks for M <= 3 (the decode token), 8 waves x 5 pairs (10 k-tiles,
+  // 40 norm-weight chunks per wave): chunks per lane = ceil(40 M / 64).
+  if (a.KT == 80 && a.M <= 3) {
+    if (a.M == 1) return launch_half_cfg<8, RBW, EPI, 5, 1>(a, stream);
+    return launch_half_cfg<8, RBW, EPI, 5, 2>(a, stream);
+  }
   if (a.KT == 80) {
     if (a.M <= 3) return launch_decode_cfg<16, RBW, EPI, 5, 1>(a, stream);
     if (a.M <= 9) return launch_decode_cfg<16, RBW, EPI, 5, 3>(a, stream);
