@@ -770,11 +770,14 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
 // the round-based prologue.
 template <int RBW, int EPI>
 hipError_t launch_rms_shape(const DecodeArgs& a, hipStream_t stream) {
-  // Half-blocks for M <= 3 (the decode token), 8 waves x 5 pairs (10 k-tiles,
-  // 40 norm-weight chunks per wave): chunks per lane = ceil(40 M / 64).
-  if (a.KT == 80 && a.M <= 3) {
+  // Half-blocks for M <= 8, 8 waves x 5 pairs (10 k-tiles, 40 norm-weight
+  // chunks per wave): chunks per lane = ceil(40 M / 64).
+  if (a.KT == 80 && a.M <= 8) {
     if (a.M == 1) return launch_half_cfg<8, RBW, EPI, 5, 1>(a, stream);
-    return launch_half_cfg<8, RBW, EPI, 5, 2>(a, stream);
+    if (a.M <= 3) return launch_half_cfg<8, RBW, EPI, 5, 2>(a, stream);
+    if (a.M == 4) return launch_half_cfg<8, RBW, EPI, 5, 3>(a, stream);
+    if (a.M <= 6) return launch_half_cfg<8, RBW, EPI, 5, 4>(a, stream);
+    return launch_half_cfg<8, RBW, EPI, 5, 5>(a, stream);
   }
   if (a.KT == 80) {
     if (a.M <= 3) return launch_decode_cfg<16, RBW, EPI, 5, 1>(a, stream);
