@@ -1,8 +1,9 @@
 // Decode attention (one new token) for gfx950: the work between the QKV and
 // o_proj projections of a Qwen3 decode layer, in one launch.
 //
-// Per (kv head j, 512-row chunk of the cache) one workgroup of 8 waves, from
-// the raw QKV projection row:
+// Per (kv head j, chunk of the rows attended) one workgroup of 8 waves, from
+// the raw QKV projection row (chunks of 128, 256, 384 or 512 rows, the
+// smallest that keeps their count at 32 or below):
 //   1. q heads jG..jG+G-1 and k head j: RMSNorm over head_dim with the q / k
 //      norm weights, then rotate-half RoPE with this position's cos / sin
 //      (src/leanstack/runtime/qwen_explicit.py:796-806, :690-716), in the
