@@ -279,13 +279,16 @@ def main() -> int:
     final_norm = (1 + 0.1 * torch.randn((G.hidden_size,), generator=gen, device=dev)).to(torch.bfloat16)
     token_step = DecodeStep(layers, norms, qk_norms, final_norm, lm_head, G, k_cache, v_cache, dev)
     token_step.hidden[0].copy_(torch.randn((1, G.hidden_size), generator=gen, device=dev).to(torch.bfloat16))
+    # One graph for every position: the attention kernels read the position
+    # from token_step.pos_dev, written before the replays.
+    token_step.set_position(0)
+    graph = stack.capture(lambda: token_step.launch())
     for pos in (320, kv_rows - 1):
-        graph = stack.capture(lambda pos=pos: token_step.launch(pos))
+        token_step.set_position(pos)
         ms = time_graph(torch, graph, steps, warmup)
         token_steps[pos] = {"us": round(ms * 1e3, 1), "tokens_per_s": round(1e3 / ms, 1)}
         log(f"decode token with attention over {pos} cached rows: {ms * 1e3:.1f} us ({1e3 / ms:.0f} tokens/s)")
-        del graph
-    del token_step, k_cache, v_cache
+    del graph, token_step, k_cache, v_cache
 
     # --- per projection kind: 36 launches of one kind per replay ------------
     per_kernel = {}

@@ -182,6 +182,23 @@ int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim,
                               float scale, void* out,
                               void* workspace, size_t ws_bytes, void* hip_stream);
 
+/* The same step with the position in device memory, for a decode step
+ * captured once as a HIP graph and replayed for every token (the caller
+ * writes the next position into *pos_device between replays): cos_table /
+ * sin_table are the whole position tables [max_seq_len][d/2] (bf16, the
+ * reference's position cache, src/leanstack/runtime/qwen_explicit.py:664-676),
+ * of which row *pos_device is used.  The launch shape does not depend on the
+ * position, so the workspace is required once max_seq_len exceeds 128.  A
+ * *pos_device outside [0, max_seq_len) leaves every buffer untouched.  Same
+ * results as lsk_decode_attention_bf16 at that position, bit for bit.
+ * Replaces the same reference code as lsk_decode_attention_bf16. */
+int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_dim,
+                                 const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                 const void* cos_table, const void* sin_table,
+                                 void* k_cache, void* v_cache, int max_seq_len, const int* pos_device,
+                                 float scale, void* out, void* workspace, size_t ws_bytes,
+                                 void* hip_stream);
+
 /* Greedy lm_head: out_idx[m] = argmax_v sum_k f32(W[v][k]) * f32(x[m][k]) for
  * m < M (M = 1..16), lowest index on ties.
  *   logits_mode  LSK_LOGITS_FP32 compares fp32 scores, as the cuTile kernel

@@ -236,11 +236,12 @@ size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_se
   return lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
 }
 
-int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim, const void* q_norm_weight,
-                              const void* k_norm_weight, float eps, const void* cos, const void* sin, void* k_cache,
-                              void* v_cache, int max_seq_len, int pos, float scale, void* out, void* workspace,
-                              size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
+namespace {
+
+// Checks shared by both attention entry points (everything but pos).
+int check_attention_args(const void* qkv, int n_q, int n_kv, int head_dim, const void* q_norm_weight,
+                         const void* k_norm_weight, float eps, const void* cos, const void* sin, void* k_cache,
+                         void* v_cache, int max_seq_len, float scale, void* out) {
   if (head_dim != lsk::kAttnHeadDim)
     return fail(LSK_ERR_INVALID, "head_dim=%d: the attention kernel is built for %d", head_dim, lsk::kAttnHeadDim);
   if (n_kv < 1 || n_kv > lsk::kAttnMaxKvHeads || n_q < n_kv || n_q % n_kv != 0 ||
@@ -255,21 +256,57 @@ int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim, 
     return fail(LSK_ERR_INVALID, "bf16 arguments must be 2-byte aligned");
   if (!aligned(k_cache, 16) || !aligned(v_cache, 16))
     return fail(LSK_ERR_INVALID, "the key and value caches must be 16-byte aligned");
-  const int max_rows = lsk::kAttnMaxRows;
-  if (max_seq_len < 1 || max_seq_len > max_rows || pos < 0 || pos >= max_seq_len)
-    return fail(LSK_ERR_INVALID, "pos=%d, max_seq_len=%d: need 0 <= pos < max_seq_len <= %d", pos, max_seq_len,
-                max_rows);
+  if (max_seq_len < 1 || max_seq_len > lsk::kAttnMaxRows)
+    return fail(LSK_ERR_INVALID, "max_seq_len=%d: need 1 <= max_seq_len <= %d", max_seq_len, lsk::kAttnMaxRows);
   if (!std::isfinite(eps) || eps < 0.f) return fail(LSK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
   if (!std::isfinite(scale)) return fail(LSK_ERR_INVALID, "scale must be finite");
-  if (pos + 1 > lsk::kAttnMinChunkRows) {
-    const size_t need = lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
-    if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 256))
-      return fail(LSK_ERR_WORKSPACE, "attending %d rows needs a workspace of %zu bytes, 256-byte aligned (got %zu)",
-                  pos + 1, need, workspace ? ws_bytes : 0);
-  }
+  return LSK_OK;
+}
+
+int check_attention_workspace(int n_q, int n_kv, int max_seq_len, int rows, const void* workspace,
+                              size_t ws_bytes) {
+  if (rows <= lsk::kAttnMinChunkRows) return LSK_OK;
+  const size_t need = lsk::attention_workspace_bytes(n_q, n_kv, max_seq_len);
+  if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 256))
+    return fail(LSK_ERR_WORKSPACE, "attending up to %d rows needs a workspace of %zu bytes, 256-byte aligned (got %zu)",
+                rows, need, workspace ? ws_bytes : 0);
+  return LSK_OK;
+}
+
+}  // namespace
+
+int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim, const void* q_norm_weight,
+                              const void* k_norm_weight, float eps, const void* cos, const void* sin, void* k_cache,
+                              void* v_cache, int max_seq_len, int pos, float scale, void* out, void* workspace,
+                              size_t ws_bytes, void* hip_stream) {
+  g_last_error.clear();
+  if (int st = check_attention_args(qkv, n_q, n_kv, head_dim, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
+                                    v_cache, max_seq_len, scale, out))
+    return st;
+  if (pos < 0 || pos >= max_seq_len)
+    return fail(LSK_ERR_INVALID, "pos=%d, max_seq_len=%d: need 0 <= pos < max_seq_len", pos, max_seq_len);
+  if (int st = check_attention_workspace(n_q, n_kv, max_seq_len, pos + 1, workspace, ws_bytes)) return st;
   hipError_t err = lsk::launch_decode_attention(qkv, n_q, n_kv, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
                                                 v_cache, max_seq_len, pos, scale, out, workspace, ws_bytes,
                                                 static_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess) return hip_fail(err, "decode attention kernel launch");
+  return LSK_OK;
+}
+
+int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_dim, const void* q_norm_weight,
+                                 const void* k_norm_weight, float eps, const void* cos_table, const void* sin_table,
+                                 void* k_cache, void* v_cache, int max_seq_len, const int* pos_device, float scale,
+                                 void* out, void* workspace, size_t ws_bytes, void* hip_stream) {
+  g_last_error.clear();
+  if (int st = check_attention_args(qkv, n_q, n_kv, head_dim, q_norm_weight, k_norm_weight, eps, cos_table,
+                                    sin_table, k_cache, v_cache, max_seq_len, scale, out))
+    return st;
+  if (pos_device == nullptr || !aligned(pos_device, 4))
+    return fail(LSK_ERR_INVALID, "pos_device must be a 4-byte aligned device int");
+  if (int st = check_attention_workspace(n_q, n_kv, max_seq_len, max_seq_len, workspace, ws_bytes)) return st;
+  hipError_t err = lsk::launch_decode_attention_at(qkv, n_q, n_kv, q_norm_weight, k_norm_weight, eps, cos_table,
+                                                   sin_table, k_cache, v_cache, max_seq_len, pos_device, scale, out,
+                                                   workspace, ws_bytes, static_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess) return hip_fail(err, "decode attention kernel launch");
   return LSK_OK;
 }

@@ -105,6 +105,8 @@ struct AttnArgs {
   unsigned partial_bytes;  // bytes of all slots of this launch
   int n_q, n_kv, s_max, pos, chunks;  // chunks of 128 * NU rows
   float eps, scale;
+  int grid_chunks;                    // workgroups per kv head in the grid (>= chunks)
+  const int* pos_ptr;                 // device-resident pos (then cos / sin are whole tables)
 };
 
 constexpr int kCoherent = 16;  // device-coherent buffer access (partials cross XCDs)
@@ -174,26 +176,44 @@ __device__ __forceinline__ void combine_chunks(const AttnArgs& a, __amdgpu_buffe
   }
 }
 
-template <int G, int NU>
-__global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) {
+// DYN: pos is read from device memory (a.pos_ptr), cos / sin are the whole
+// position tables ([s_max][d/2]), and the chunk size and count follow from
+// pos here; the grid holds the most chunks max_seq_len can need and the
+// workgroups past this pos's count leave at once.  A pos outside
+// [0, s_max) leaves every buffer untouched.
+template <int G, int NU, bool DYN>
+__global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs args) {
   static_assert(G >= 1 && G <= 16, "q heads per kv head are the MFMA B columns");
   constexpr int kGroups = NU;              // 16-row groups per wave
-  constexpr int kRows = 16 * kWaves * NU;  // rows per workgroup: 128 NU
+  constexpr int kRows = 16 * kWaves * NU;  // rows per workgroup at most: 128 NU
   constexpr int kMaxChunks = kAttnMaxChunks;
-  const int j = blockIdx.x / a.chunks;
-  const int ci = blockIdx.x - j * a.chunks;
+  AttnArgs a = args;
+  int rows = kRows;  // rows per chunk
+  if constexpr (DYN) {
+    const int pos = *args.pos_ptr;
+    if (pos < 0 || pos >= a.s_max) return;
+    a.pos = pos;
+    a.cos += (size_t)pos * (kHeadDim / 2);
+    a.sin += (size_t)pos * (kHeadDim / 2);
+    const int units = (pos + kAttnMinChunkRows) / kAttnMinChunkRows;  // ceil((pos + 1) / 128)
+    rows = kAttnMinChunkRows * ((units + kAttnMaxChunks - 1) / kAttnMaxChunks);
+    a.chunks = (pos + rows) / rows;  // ceil((pos + 1) / rows)
+  }
+  const int j = blockIdx.x / a.grid_chunks;
+  const int ci = blockIdx.x - j * a.grid_chunks;
+  if (ci >= a.chunks) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int c = lane & 15;
   const int L = a.pos + 1;
-  const int row0 = ci * kRows;
+  const int row0 = ci * rows;
   // Wave w owns the chunk's 16-row groups w, w + 8, w + 16, ...: group u of
   // the wave starts at chunk row lb(u) = 16 (w + 8u).  Groups past the last
   // row are skipped, so short contexts cost little and the waves share the
   // rows evenly.
   auto lb = [&](int u) { return 16 * (wave + kWaves * u); };
-  const bool has_new = a.pos >= row0 && a.pos < row0 + kRows;
+  const bool has_new = a.pos >= row0 && a.pos < row0 + rows;
 
   __shared__ __align__(16) __bf16 qs[16][kHeadDim];     // rotated q heads; rows >= G are zero
   __shared__ __align__(16) __bf16 kv_new[2][kHeadDim];  // this token's rotated k and its v
@@ -247,14 +267,15 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       bf16x8_t v = {};
-      if (t < a.pos) v = *reinterpret_cast<const bf16x8_t*>(kbase + (size_t)t * kHeadDim + 32 * kt + 8 * g);
+      if (t < a.pos && lb(u) < rows)
+        v = *reinterpret_cast<const bf16x8_t*>(kbase + (size_t)t * kHeadDim + 32 * kt + 8 * g);
       kf[u][kt] = v;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tv = row0 + lb(u) + 4 * i + g;
       bf16x8_t v = {};
-      if (tv < a.pos) v = *reinterpret_cast<const bf16x8_t*>(vbase + (size_t)tv * kHeadDim + 8 * c);
+      if (tv < a.pos && lb(u) < rows) v = *reinterpret_cast<const bf16x8_t*>(vbase + (size_t)tv * kHeadDim + 8 * c);
       vf[u][i] = v;
     }
   }
@@ -312,7 +333,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   for (int kt = 0; kt < 4; ++kt) qf[kt] = *reinterpret_cast<const bf16x8_t*>(&qs[c][32 * kt + 8 * g]);
 #pragma unroll
   for (int u = 0; u < kGroups; ++u) {
-    if (row0 + lb(u) >= L) break;
+    if (lb(u) >= rows || row0 + lb(u) >= L) break;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u][kt], qf[kt], acc, 0, 0, 0);
@@ -326,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   // ---- chunk softmax state per head over its filled rows n (up to
   // kRows / 64 per lane, summed in row order within a lane, then across
   // lanes); the rows past the last are never read again.
-  const int n = min(kRows, L - row0);
+  const int n = min(rows, L - row0);
   for (int h = wave; h < G; h += kWaves) {
     float sv[kRows / 64];
     float mx = -__builtin_huge_valf();
@@ -365,7 +386,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
     for (int e = 0; e < 8; ++e) acc8[h][e] = 0.f;
 #pragma unroll
   for (int u = 0; u < kGroups; ++u) {
-    if (row0 + lb(u) >= L) break;
+    if (lb(u) >= rows || row0 + lb(u) >= L) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tl = lb(u) + 4 * i + g;  // row within the chunk
@@ -452,9 +473,9 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs a) 
   if (threadIdx.x == 0) __hip_atomic_store(a.counters + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int G, int NU>
+template <int G, int NU, bool DYN = false>
 hipError_t launch_gu(const AttnArgs& a, hipStream_t stream) {
-  decode_attention_kernel<G, NU><<<dim3(a.n_kv * a.chunks), dim3(kThreads), 0, stream>>>(a);
+  decode_attention_kernel<G, NU, DYN><<<dim3(a.n_kv * a.grid_chunks), dim3(kThreads), 0, stream>>>(a);
   return hipGetLastError();
 }
 
@@ -490,10 +511,11 @@ size_t attention_workspace_bytes(int n_q, int n_kv, int max_seq_len) {
 
 bool attention_group_supported(int group) { return group == 1 || group == 2 || group == 4 || group == 8; }
 
-hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w,
-                                   float eps, const void* cos, const void* sin, void* k_cache, void* v_cache,
-                                   int s_max, int pos, float scale, void* out, void* workspace, size_t ws_bytes,
-                                   hipStream_t stream) {
+namespace {
+
+AttnArgs common_args(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w, float eps,
+                     const void* cos, const void* sin, void* k_cache, void* v_cache, int s_max, float scale,
+                     void* out, void* workspace, size_t ws_bytes) {
   AttnArgs a;
   a.qkv = static_cast<const __bf16*>(qkv);
   a.q_norm_w = static_cast<const __bf16*>(q_norm_w);
@@ -506,10 +528,10 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
   a.n_q = n_q;
   a.n_kv = n_kv;
   a.s_max = s_max;
-  a.pos = pos;
-  const int rows = attention_chunk_rows(pos + 1);
-  const int nu = rows / kAttnMinChunkRows;
-  a.chunks = (pos + 1 + rows - 1) / rows;
+  a.pos = 0;
+  a.chunks = 1;
+  a.grid_chunks = 1;
+  a.pos_ptr = nullptr;
   a.eps = eps;
   a.scale = scale;
   auto* ws = static_cast<unsigned char*>(workspace);
@@ -517,6 +539,22 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
   a.partials = ws != nullptr ? ws + kAttnPartialsOffset : nullptr;
   const size_t pb = ws_bytes > kAttnPartialsOffset ? ws_bytes - kAttnPartialsOffset : 0;
   a.partial_bytes = (unsigned)(pb < 0x7fffffffu ? pb : 0x7fffffffu);
+  return a;
+}
+
+}  // namespace
+
+hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w,
+                                   float eps, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                                   int s_max, int pos, float scale, void* out, void* workspace, size_t ws_bytes,
+                                   hipStream_t stream) {
+  AttnArgs a = common_args(qkv, n_q, n_kv, q_norm_w, k_norm_w, eps, cos, sin, k_cache, v_cache, s_max, scale, out,
+                           workspace, ws_bytes);
+  a.pos = pos;
+  const int rows = attention_chunk_rows(pos + 1);
+  const int nu = rows / kAttnMinChunkRows;
+  a.chunks = (pos + 1 + rows - 1) / rows;
+  a.grid_chunks = a.chunks;
   switch (n_q / n_kv) {
     case 1:
       return launch_g<1>(a, nu, stream);
@@ -526,6 +564,33 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
       return launch_g<4>(a, nu, stream);
     case 8:
       return launch_g<8>(a, nu, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+int attention_grid_chunks(int max_seq_len) {
+  const int most = (max_seq_len + kAttnMinChunkRows - 1) / kAttnMinChunkRows;
+  return most < kAttnMaxChunks ? most : kAttnMaxChunks;
+}
+
+hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w,
+                                      float eps, const void* cos_table, const void* sin_table, void* k_cache,
+                                      void* v_cache, int s_max, const int* pos_device, float scale, void* out,
+                                      void* workspace, size_t ws_bytes, hipStream_t stream) {
+  AttnArgs a = common_args(qkv, n_q, n_kv, q_norm_w, k_norm_w, eps, cos_table, sin_table, k_cache, v_cache, s_max,
+                           scale, out, workspace, ws_bytes);
+  a.pos_ptr = pos_device;
+  a.grid_chunks = attention_grid_chunks(s_max);
+  switch (n_q / n_kv) {
+    case 1:
+      return launch_gu<1, 4, true>(a, stream);
+    case 2:
+      return launch_gu<2, 4, true>(a, stream);
+    case 4:
+      return launch_gu<4, 4, true>(a, stream);
+    case 8:
+      return launch_gu<8, 4, true>(a, stream);
     default:
       return hipErrorInvalidValue;
   }

@@ -131,6 +131,15 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
                                    int s_max, int pos, float scale, void* out, void* workspace, size_t ws_bytes,
                                    hipStream_t stream);
 
+// The same with pos read from device memory (pos_device, one int) and cos /
+// sin the whole position tables [s_max][d/2]: one launch shape for every
+// position, so a captured graph serves each token.  The grid holds the most
+// chunks max_seq_len can need; a pos outside [0, s_max) changes nothing.
+hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w,
+                                      float eps, const void* cos_table, const void* sin_table, void* k_cache,
+                                      void* v_cache, int s_max, const int* pos_device, float scale, void* out,
+                                      void* workspace, size_t ws_bytes, hipStream_t stream);
+
 // Number of workgroups (= argmax partials per row) the lm_head kernel uses.
 int lm_head_partials(int V);
 

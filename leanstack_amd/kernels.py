@@ -178,17 +178,25 @@ def attention_workspace(device: torch.device, n_q: int, n_kv: int, head_dim: int
 
 
 def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
-                     cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: int,
-                     scale: float, *, num_attention_heads: int, num_key_value_heads: int,
+                     cos: torch.Tensor, sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     pos: int | torch.Tensor, scale: float, *, num_attention_heads: int, num_key_value_heads: int,
                      out: torch.Tensor | None = None, workspace: torch.Tensor | str = "auto") -> torch.Tensor:
     """One decode token of one layer between QKV and o_proj: per-head q/k
     RMSNorm and RoPE of the raw QKV row, k and v written to row `pos` of the
     layer's caches ([n_kv, max_seq_len, d] bf16, batch 1), and GQA attention
     over rows 0..pos.  Returns out [n_q * d] bf16.  The caller advances its
     cache cursor.  workspace: "auto" (attention_workspace), or a zero-filled
-    uint8 device tensor of lsk_attention_workspace_bytes() bytes."""
+    uint8 device tensor of lsk_attention_workspace_bytes() bytes.
+
+    pos: an int (cos / sin are this position's rows, d/2 values each), or a
+    one-element int32 device tensor read by the kernel (cos / sin are then the
+    whole [max_seq_len, d/2] tables): one launch for any position, so a
+    captured HIP graph can be replayed token after token with the caller
+    writing the next position into that tensor.  Out-of-range device
+    positions change nothing."""
     lib = _lib.load()
     n_q, n_kv = num_attention_heads, num_key_value_heads
+    on_device = isinstance(pos, torch.Tensor)
     for t, what in ((qkv, "qkv"), (q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"), (cos, "cos"),
                     (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _require_device(t, what)
@@ -199,11 +207,17 @@ def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
                          f"{tuple(k_cache.shape)} / {tuple(v_cache.shape)}")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("k_cache / v_cache must be contiguous")
-    d = k_cache.shape[2]
+    d, s_max = k_cache.shape[2], k_cache.shape[1]
     if qkv.numel() != (n_q + 2 * n_kv) * d:
         raise ValueError(f"qkv has {qkv.numel()} values, expected {(n_q + 2 * n_kv) * d}")
-    if q_norm_weight.numel() != d or k_norm_weight.numel() != d or cos.numel() != d // 2 or sin.numel() != d // 2:
-        raise ValueError(f"norm weights must hold {d} values and cos / sin {d // 2} (this position's row)")
+    rope_len = s_max * (d // 2) if on_device else d // 2
+    if q_norm_weight.numel() != d or k_norm_weight.numel() != d or cos.numel() != rope_len or sin.numel() != rope_len:
+        where = f"the whole [{s_max}, {d // 2}] tables" if on_device else "this position's row"
+        raise ValueError(f"norm weights must hold {d} values and cos / sin {rope_len} ({where})")
+    if on_device:
+        _require_device(pos, "pos")
+        if pos.dtype != torch.int32 or pos.numel() != 1:
+            raise ValueError("a device pos must be a one-element int32 tensor")
     flat = [t.reshape(-1).contiguous() for t in (qkv, q_norm_weight, k_norm_weight, cos, sin)]
     if out is None:
         out = torch.empty((n_q * d,), device=qkv.device, dtype=torch.bfloat16)
@@ -212,15 +226,18 @@ def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
     if isinstance(workspace, str):
         if workspace != "auto":
             raise ValueError(f"workspace must be 'auto' or a tensor, not {workspace!r}")
-        workspace = attention_workspace(qkv.device, n_q, n_kv, d, k_cache.shape[1])
+        workspace = attention_workspace(qkv.device, n_q, n_kv, d, s_max)
     _require_device(workspace, "workspace")
-    status = lib.lsk_decode_attention_bf16(
-        flat[0].data_ptr(), n_q, n_kv, d, flat[1].data_ptr(), flat[2].data_ptr(), float(eps),
-        flat[3].data_ptr(), flat[4].data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[1], int(pos),
-        float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-        stream_handle(),
-    )
-    _lib.check(status, "lsk_decode_attention_bf16")
+    common = (flat[0].data_ptr(), n_q, n_kv, d, flat[1].data_ptr(), flat[2].data_ptr(), float(eps),
+              flat[3].data_ptr(), flat[4].data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), s_max)
+    tail = (float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            stream_handle())
+    if on_device:
+        status = lib.lsk_decode_attention_at_bf16(*common, pos.data_ptr(), *tail)
+        _lib.check(status, "lsk_decode_attention_at_bf16")
+    else:
+        status = lib.lsk_decode_attention_bf16(*common, int(pos), *tail)
+        _lib.check(status, "lsk_decode_attention_bf16")
     return out
 
 

@@ -146,8 +146,10 @@ class DecodeStep:
     attention kernel (q/k norms, RoPE, cache append, GQA attention), o_proj
     + residual, post_attention_layernorm + gate_up + SiLU*up, down +
     residual; then the final RMSNorm and the lm_head argmax.  All buffers are
-    fixed, so the launch sequence can be captured as one HIP graph; the
-    position is part of what is captured.
+    fixed, so the launch sequence can be captured as one HIP graph.
+    launch(pos) bakes the position into the launches; launch() reads it from
+    the device (self.pos_dev, set with set_position), so one captured graph
+    serves every token of a sequence.
 
     norms: [n, 2, H] (input / post-attention), qk_norms: [n, 2, d] (q / k),
     k_cache / v_cache: [n, n_kv, max_seq_len, d]."""
@@ -178,18 +180,30 @@ class DecodeStep:
                                                                g.head_dim, max_seq)
         self.attn_ws = torch.zeros(ws_bytes, device=device, dtype=torch.uint8)  # left zeroed by every launch
         self.token = torch.empty((1,), device=device, dtype=torch.long)
+        self.pos_dev = torch.zeros((1,), device=device, dtype=torch.int32)
 
-    def launch(self, pos: int) -> None:
+    def set_position(self, pos: int) -> None:
+        """Write the position launch() reads, ordered on the current stream
+        before whatever is enqueued next (a graph replay included)."""
+        if not 0 <= pos < self.k_cache.shape[2]:
+            raise ValueError(f"pos={pos} outside 0..{self.k_cache.shape[2] - 1}")
+        self.pos_dev.fill_(pos)
+
+    def launch(self, pos: int | None = None) -> None:
         """Enqueue the token at position `pos` (rows 0..pos-1 of every layer's
-        cache are the context); its input is self.hidden[0], its output
-        token self.token."""
+        cache are the context), or, with pos None, at the position in
+        self.pos_dev; its input is self.hidden[0], its output token
+        self.token."""
         g = self.g
-        cos, sin = self.cos[pos], self.sin[pos]
+        if pos is None:
+            cos, sin, where = self.cos, self.sin, self.pos_dev
+        else:
+            cos, sin, where = self.cos[pos], self.sin[pos], pos
         for l, p in enumerate(self.layers):
             x, y = self.hidden[l % 2], self.hidden[(l + 1) % 2]
             kernels.rmsnorm_linear(x, self.norms[l, 0], self.eps, p.qkv, out=self.qkv)
             kernels.decode_attention(self.qkv, self.qk_norms[l, 0], self.qk_norms[l, 1], self.eps, cos, sin,
-                                     self.k_cache[l], self.v_cache[l], pos, self.scale,
+                                     self.k_cache[l], self.v_cache[l], where, self.scale,
                                      num_attention_heads=g.num_attention_heads,
                                      num_key_value_heads=g.num_key_value_heads, out=self.attn,
                                      workspace=self.attn_ws)

@@ -116,6 +116,25 @@ def test_decode_attention_rejects_before_launch(kwargs, code):
     assert _lib.last_error()
 
 
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(pos_ptr=0), _lib.ERR_INVALID),         # no device position
+    (dict(pos_ptr=FAKE + 2), _lib.ERR_INVALID),  # not 4-byte aligned
+    (dict(ws=0), _lib.ERR_WORKSPACE),            # the launch shape covers max_seq_len rows
+    (dict(s=20000), _lib.ERR_INVALID),
+    (dict(d=64), _lib.ERR_INVALID),
+    (dict(eps=float("nan")), _lib.ERR_INVALID),
+])
+def test_decode_attention_at_rejects_before_launch(kwargs, code):
+    a = dict(pos_ptr=FAKE, s=4096, d=128, eps=1e-6, ws=FAKE)
+    a.update(kwargs)
+    lib = _lib.load()
+    status = lib.lsk_decode_attention_at_bf16(FAKE, 32, 8, a["d"], FAKE, FAKE, a["eps"], FAKE, FAKE, FAKE, FAKE,
+                                              a["s"], a["pos_ptr"] or None, 128 ** -0.5, FAKE, a["ws"] or None,
+                                              1 << 30, None)
+    assert status == code, _lib.last_error()
+    assert _lib.last_error()
+
+
 def test_attention_workspace_bytes():
     """Counters for 64 kv heads, then one (m, l, acc) slot of 4 * (2G + 128G)
     bytes per (kv head, chunk); at most 32 chunks of at least 128 rows."""

@@ -81,6 +81,71 @@ def test_decode_attention_long_cache(gpu, pos):
     _check_case(G.num_attention_heads, G.num_key_value_heads, 16384, pos, seed=9300 + pos)
 
 
+def _same_bits(a, b):
+    """bf16 tensors equal bit for bit (NaN payloads included)."""
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def _device_pos_case(s_max, positions, seed):
+    """The device-position entry point against the host-position one, launch
+    by launch on the same inputs: outputs and caches bit for bit."""
+    n_q, n_kv = G.num_attention_heads, G.num_key_value_heads
+    gen = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn((n_q + 2 * n_kv) * D, generator=gen) * 2).to(torch.bfloat16).to(DEV)
+    qn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(DEV)
+    kn = (1 + 0.2 * torch.randn(D, generator=gen)).to(torch.bfloat16).to(DEV)
+    ang = torch.rand((s_max, D // 2), generator=gen) * 50
+    cos_t, sin_t = ang.cos().to(torch.bfloat16).to(DEV), ang.sin().to(torch.bfloat16).to(DEV)
+    kc = torch.randn((n_kv, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    vc = torch.randn((n_kv, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    pos_dev = torch.zeros((1,), dtype=torch.int32, device=DEV)
+    ws_a = torch.zeros(_lib.load().lsk_attention_workspace_bytes(n_q, n_kv, D, s_max), dtype=torch.uint8, device=DEV)
+    ws_b = torch.zeros_like(ws_a)
+    k1, v1, k2, v2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    for pos in positions:
+        a = kernels.decode_attention(qkv, qn, kn, EPS, cos_t[pos], sin_t[pos], k1, v1, pos, D ** -0.5,
+                                     num_attention_heads=n_q, num_key_value_heads=n_kv, workspace=ws_a)
+        pos_dev.fill_(pos)
+        b = kernels.decode_attention(qkv, qn, kn, EPS, cos_t, sin_t, k2, v2, pos_dev, D ** -0.5,
+                                     num_attention_heads=n_q, num_key_value_heads=n_kv, workspace=ws_b)
+        torch.cuda.synchronize()
+        assert not torch.isnan(b).any(), pos
+        assert _same_bits(a, b), f"pos={pos}: device-position output differs"
+        assert _same_bits(k1, k2) and _same_bits(v1, v2), f"pos={pos}: caches differ"
+    assert not ws_b[:256].any(), "the arrival counters are left zero"
+
+
+def test_decode_attention_device_position(gpu):
+    """Positions in device memory at every chunk-rule regime up to 4096 rows."""
+    _device_pos_case(4096, [0, 1, 127, 128, 129, 511, 1000, 2047, 3072, 4095], 9400)
+
+
+def test_decode_attention_device_position_long_cache(gpu):
+    """A 16384-row cache: chunks of 256, 384 and 512 rows from the device pos."""
+    _device_pos_case(16384, [4096, 8192, 12288, 16383, 3], 9401)
+
+
+def test_decode_attention_device_position_out_of_range(gpu):
+    """A device pos outside [0, max_seq_len) leaves the output, the caches and
+    the workspace untouched."""
+    n_q, n_kv, s_max = 8, 2, 256
+    gen = torch.Generator().manual_seed(9402)
+    qkv = torch.randn((n_q + 2 * n_kv) * D, generator=gen).to(torch.bfloat16).to(DEV)
+    ones = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    tab = torch.ones((s_max, D // 2), dtype=torch.bfloat16, device=DEV)
+    kc = torch.randn((n_kv, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    vc = kc.clone()
+    k0, v0 = kc.clone(), vc.clone()
+    ws = torch.zeros(_lib.load().lsk_attention_workspace_bytes(n_q, n_kv, D, s_max), dtype=torch.uint8, device=DEV)
+    for bad in (s_max, -1, 1 << 30):
+        out = torch.full((n_q * D,), 7.0, dtype=torch.bfloat16, device=DEV)
+        pos_dev = torch.full((1,), bad, dtype=torch.int32, device=DEV)
+        kernels.decode_attention(qkv, ones, ones, EPS, tab, tab, kc, vc, pos_dev, D ** -0.5, num_attention_heads=n_q,
+                                 num_key_value_heads=n_kv, out=out, workspace=ws)
+        torch.cuda.synchronize()
+        assert (out == 7.0).all() and torch.equal(kc, k0) and torch.equal(vc, v0) and not ws.any(), bad
+
+
 @pytest.mark.parametrize("n_q", [2, 4, 16])
 @pytest.mark.parametrize("pos", [0, 100, 511])
 def test_decode_attention_group_sizes(gpu, n_q, pos):
@@ -234,3 +299,52 @@ def test_decode_step_two_layers_and_head(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert step.token.item() == token
+
+
+def test_decode_step_one_graph_for_every_position(gpu):
+    """DecodeStep.launch() with the position in device memory: one graph,
+    captured once, replayed at positions 3, 4, 5 (set_position between
+    replays, the output hidden fed back as the next input) gives the tokens,
+    hidden states and caches of per-position eager launches, bit for bit."""
+    from leanstack_amd.stack import DecodeStep, LayerProjections
+
+    n_layers, s_max = 2, 200
+    layers_cpu, layers = [], []
+    for l in range(n_layers):
+        w, layer = _layer(9700 + 10 * l)
+        layers_cpu.append(w)
+        layers.append(LayerProjections(layer.attention.qkv_proj_weight, layer.attention.o_proj_weight,
+                                       layer.mlp.gate_up_proj_weight, layer.mlp.down_proj_weight))
+    norms = torch.stack([torch.stack((w["in_ln"], w["post_ln"])) for w in layers_cpu]).to(DEV)
+    qk = torch.stack([torch.stack((w["qn"], w["kn"])) for w in layers_cpu]).to(DEV)
+    gen = torch.Generator().manual_seed(9799)
+    final = (1 + 0.1 * torch.randn(G.hidden_size, generator=gen)).to(torch.bfloat16).to(DEV)
+    lm = PackedWeight.from_rowmajor(weight(G.vocab_size, G.hidden_size, seed=9798).to(DEV))
+    kc = torch.randn((n_layers, G.num_key_value_heads, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    vc = torch.randn((n_layers, G.num_key_value_heads, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    hidden = (torch.randn(G.hidden_size, generator=gen) * 3).to(torch.bfloat16).to(DEV)
+    eager = DecodeStep(layers, norms, qk, final, lm, G, kc.clone(), vc.clone(), DEV)
+    graphed = DecodeStep(layers, norms, qk, final, lm, G, kc.clone(), vc.clone(), DEV)
+    graphed.set_position(3)
+    graphed.hidden[0, 0] = hidden
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        graphed.launch()
+    # capture ran nothing: reset what the graph will write, then replay per position
+    graphed.k_cache.copy_(kc)
+    graphed.v_cache.copy_(vc)
+    h_eager = h_graph = hidden
+    for pos in (3, 4, 5):
+        eager.hidden[0, 0] = h_eager
+        eager.launch(pos)
+        graphed.hidden[0, 0] = h_graph
+        graphed.set_position(pos)
+        graph.replay()
+        torch.cuda.synchronize()
+        out_e, out_g = eager.hidden[n_layers % 2, 0].clone(), graphed.hidden[n_layers % 2, 0].clone()
+        assert _same_bits(out_e, out_g), f"pos {pos}: hidden differs"
+        assert eager.token.item() == graphed.token.item(), f"pos {pos}: token differs"
+        h_eager, h_graph = out_e, out_g
+    assert _same_bits(eager.k_cache, graphed.k_cache) and _same_bits(eager.v_cache, graphed.v_cache)
+    with pytest.raises(ValueError):
+        graphed.set_position(s_max)
