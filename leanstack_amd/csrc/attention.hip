@@ -480,6 +480,22 @@ hipError_t launch_gu(const AttnArgs& a, hipStream_t stream) {
 }
 
 template <int G>
+hipError_t launch_dyn(const AttnArgs& a, int nu, hipStream_t stream) {
+  switch (nu) {
+    case 1:
+      return launch_gu<G, 1, true>(a, stream);
+    case 2:
+      return launch_gu<G, 2, true>(a, stream);
+    case 3:
+      return launch_gu<G, 3, true>(a, stream);
+    case 4:
+      return launch_gu<G, 4, true>(a, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+template <int G>
 hipError_t launch_g(const AttnArgs& a, int nu, hipStream_t stream) {
   switch (nu) {
     case 1:
@@ -582,15 +598,18 @@ hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const 
                            scale, out, workspace, ws_bytes);
   a.pos_ptr = pos_device;
   a.grid_chunks = attention_grid_chunks(s_max);
+  // Chunks never exceed the size max_seq_len rows need (the rule grows with
+  // the rows attended), so that size fixes the kernel's groups per wave.
+  const int nu = attention_chunk_rows(s_max) / kAttnMinChunkRows;
   switch (n_q / n_kv) {
     case 1:
-      return launch_gu<1, 4, true>(a, stream);
+      return launch_dyn<1>(a, nu, stream);
     case 2:
-      return launch_gu<2, 4, true>(a, stream);
+      return launch_dyn<2>(a, nu, stream);
     case 4:
-      return launch_gu<4, 4, true>(a, stream);
+      return launch_dyn<4>(a, nu, stream);
     case 8:
-      return launch_gu<8, 4, true>(a, stream);
+      return launch_dyn<8>(a, nu, stream);
     default:
       return hipErrorInvalidValue;
   }
