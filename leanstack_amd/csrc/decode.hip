@@ -23,6 +23,7 @@
 
 #include <climits>
 #include <mutex>
+#include <type_traits>
 
 #include "lsk_internal.h"
 
@@ -316,6 +317,80 @@ __device__ __forceinline__ void accumulate_rows_rms_dense(f32x4_t (&acc)[RBW], c
   }
 }
 
+// Bytes of one wave's area when its slice of x is staged: the M rows of the
+// slice (row stride U*32+8 bf16), and at least the RBW partial tiles of the
+// cross-wave sum that reuse the area.
+__host__ __device__ constexpr int staged_wave_bytes(int U, int M, int RBW) {
+  return M * (U * 32 + 8) * 2 > RBW * 1024 ? M * (U * 32 + 8) * 2 : RBW * 1024;
+}
+
+// NORM value of the kernels' staged-activation form with NC chunks per lane
+// (NORM = 0: fragments loaded per tile; > 0 and -1: the RMSNorm prologues).
+constexpr int staged_x(int nc) { return -1 - nc; }
+
+// Single-round accumulate_rows with the wave's slice of x -- M rows x U*32
+// values, M*U*4 chunks of 8 -- loaded densely (NC chunks per lane, one
+// request per chunk) and staged in the wave's LDS area, then read back as B
+// fragments.  Loading the fragments per tile instead makes every lane of
+// every wave request 16 bytes per k-tile, padding columns included: at M = 1
+// as many vector-memory requests as the weight tiles themselves.  HALF: the
+// half-block fragment order (see accumulate_rows_rms_dense).  No barrier:
+// each wave reads only its own area.
+template <int NW, int RBW, int U, int NC, bool HALF>
+__device__ __forceinline__ void accumulate_rows_staged(f32x4_t (&acc)[RBW], const bf16x8_t* __restrict__ wt,
+                                                       const __bf16* __restrict__ x, int ldx, int M, int KT, int kb,
+                                                       int wave, int lane) {
+  constexpr int kRowChunks = U * 4;
+  constexpr int kRowStride = U * 32 + 8;
+  __bf16* xs = reinterpret_cast<__bf16*>(rms_lds + (size_t)wave * staged_wave_bytes(U, M, RBW));
+  const int C = M * kRowChunks;
+  const int m = lane & 15;
+  const int g = lane >> 4;
+  bf16x8_t xd[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + 64 * i, C - 1);  // lanes past the last chunk reload it
+    const int mc = c / kRowChunks;
+    const int j = c - mc * kRowChunks;
+    xd[i] = *reinterpret_cast<const bf16x8_t*>(x + (size_t)mc * ldx + (kb * 4 + j) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int kLoads = HALF ? U / 2 : U;
+  bf16x8_t wv[kLoads][RBW];
+#pragma unroll
+  for (int u = 0; u < kLoads; ++u) {
+#pragma unroll
+    for (int r = 0; r < RBW; ++r)
+      wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kb + (HALF ? 2 * u : u)) * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = min(lane + 64 * i, C - 1);
+    const int mc = c / kRowChunks;
+    const int j = c - mc * kRowChunks;
+    *reinterpret_cast<bf16x8_t*>(xs + mc * kRowStride + j * 8) = xd[i];
+  }
+  if constexpr (HALF) {
+    const int hi = m >= M && m < 2 * M ? 1 : 0;
+    const int row = m < M ? m : (hi ? m - M : M - 1);
+#pragma unroll
+    for (int u = 0; u < kLoads; ++u) {
+      const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + row * kRowStride + (2 * u + hi) * 32 + g * 8);
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+    }
+  } else {
+    const int mr = m < M ? m : M - 1;  // padding columns: finite, never stored
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + mr * kRowStride + u * 32 + g * 8);
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+    }
+  }
+}
+
 // Round-based accumulate_rows with the RMSNorm prologue (any K): a first pass
 // over the wave's activation fragments (cache hits) gives r, then the rounds
 // run as in accumulate_rows with each fragment scaled before its multiply.
@@ -430,13 +505,18 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
   static_assert(NORM <= 0 || U > 0, "the dense RMSNorm prologue is single-round");
-  static_assert(NORM >= 0 || U == 0, "the per-lane RMSNorm prologue is round-based");
+  static_assert(NORM != -1 || U == 0, "the per-lane RMSNorm prologue is round-based");
+  static_assert(NORM >= -1 || U > 0, "staged activations are single-round");
   if constexpr (NORM > 0) {
     accumulate_rows_rms_dense<NW, RBW, U, NORM>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w), M, KT,
                                                 kb, wave, lane, eps);
-  } else if constexpr (NORM < 0) {
+  } else if constexpr (NORM == -1) {
     const bf16x8_t* nrow = reinterpret_cast<const bf16x8_t*>(norm_w) + g;
     accumulate_rows_rms<NW, RBW>(acc, wt, xrow, nrow, m_active, KT, kb, ke, wave, lane, eps);
+  } else if constexpr (NORM < -1) {
+    (void)norm_w;
+    (void)eps;
+    accumulate_rows_staged<NW, RBW, U, -1 - NORM, false>(acc, wt, x, ldx, M, KT, kb, wave, lane);
   } else {
     (void)norm_w;
     (void)eps;
@@ -445,6 +525,8 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 
   if constexpr (NORM > 0) {
     if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NORM, M, RBW))) return;
+  } else if constexpr (NORM < -1) {
+    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RBW))) return;
   } else {
     if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
   }
@@ -609,7 +691,7 @@ constexpr size_t kDefaultDynamicLds = 64 * 1024;
 template <int NW, int RBW, int EPI, int U, int NORM>
 hipError_t launch_decode_cfg(const DecodeArgs& a, hipStream_t stream) {
   auto* kernel = decode_linear_kernel<NW, RBW, EPI, U, NORM>;
-  size_t lds = 0;
+  size_t lds = NORM < -1 ? (size_t)NW * staged_wave_bytes(U, a.M, RBW) : 0;
   if constexpr (NORM > 0) {
     lds = (size_t)NW * rms_wave_bytes(U, NORM, a.M, RBW);
     if (lds > kDefaultDynamicLds) {
@@ -669,6 +751,13 @@ __global__ __launch_bounds__(NW * 64) void decode_half_kernel(
     accumulate_rows_rms_dense<NW, RBW, 2 * U, NORM, true>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w),
                                                           M, KT, 2 * pb, wave, lane, eps);
     if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(2 * U, NORM, M, RBW))) return;
+  } else if constexpr (NORM < -1) {
+    (void)xrow;
+    (void)keep;
+    (void)norm_w;
+    (void)eps;
+    accumulate_rows_staged<NW, RBW, 2 * U, -1 - NORM, true>(acc, wt, x, ldx, M, KT, 2 * pb, wave, lane);
+    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(2 * U, M, RBW))) return;
   } else {
     (void)norm_w;
     (void)eps;
@@ -722,11 +811,40 @@ __global__ __launch_bounds__(NW * 64) void decode_half_kernel(
 
 template <int NW, int RBW, int EPI, int U, int NORM = 0>
 hipError_t launch_half_cfg(const DecodeArgs& a, hipStream_t stream) {
-  const size_t lds = NORM > 0 ? (size_t)NW * rms_wave_bytes(2 * U, NORM, a.M, RBW) : 0;
+  const size_t lds = NORM > 0    ? (size_t)NW * rms_wave_bytes(2 * U, NORM, a.M, RBW)
+                     : NORM < -1 ? (size_t)NW * staged_wave_bytes(2 * U, a.M, RBW)
+                                 : 0;
   decode_half_kernel<NW, RBW, EPI, U, NORM><<<dim3(a.NB / RBW * 2), dim3(NW * 64), lds, stream>>>(
       static_cast<const bf16x8_t*>(a.w), static_cast<const __bf16*>(a.x), a.ldx, static_cast<__bf16*>(a.y), a.ldy,
       static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT, static_cast<const __bf16*>(a.norm_w), a.eps);
   return hipGetLastError();
+}
+
+// The staged-activation form with NC (1..6) chunks per lane; HALF selects
+// decode_half_kernel (U = pairs per wave), else decode_linear_kernel.
+template <int NW, int RBW, int EPI, int U, bool HALF>
+hipError_t launch_staged(const DecodeArgs& a, int nc, hipStream_t stream) {
+  auto go = [&](auto tag) -> hipError_t {
+    constexpr int kNorm = staged_x(decltype(tag)::value);
+    if constexpr (HALF) return launch_half_cfg<NW, RBW, EPI, U, kNorm>(a, stream);
+    else return launch_decode_cfg<NW, RBW, EPI, U, kNorm>(a, stream);
+  };
+  switch (nc) {
+    case 1:
+      return go(std::integral_constant<int, 1>{});
+    case 2:
+      return go(std::integral_constant<int, 2>{});
+    case 3:
+      return go(std::integral_constant<int, 3>{});
+    case 4:
+      return go(std::integral_constant<int, 4>{});
+    case 5:
+      return go(std::integral_constant<int, 5>{});
+    case 6:
+      return go(std::integral_constant<int, 6>{});
+    default:
+      return hipErrorInvalidValue;
+  }
 }
 
 // Shape dispatch: the Qwen3-4B K values get single-round instantiations
@@ -740,6 +858,21 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
   // 55 us (3.6 %) faster per step than 16-row workgroups.  o_proj and down
   // (160 row-blocks) measured slower as halves: 320 workgroups leave 64 CUs
   // with two.
+  // Activations staged through LDS (staged_x(NC), NC = chunks per lane of
+  // the wave's M * 4 * k-tiles chunks) wherever the registers and 64 KB of
+  // LDS allow: QKV for every M <= 8, gate_up (4 waves x 10 pairs up to
+  // M = 2, then 8 waves x 5), o_proj up to M = 6, down up to M = 3.
+  if (a.KT == 80 && a.M <= 8) {
+    if constexpr (RBW == 1) return launch_staged<8, RBW, EPI, 5, true>(a, (40 * a.M + 63) / 64, stream);
+    if constexpr (RBW == 2) {
+      if (a.M <= 2) return launch_staged<4, RBW, EPI, 10, true>(a, (80 * a.M + 63) / 64, stream);
+      return launch_staged<8, RBW, EPI, 5, true>(a, (40 * a.M + 63) / 64, stream);
+    }
+  }
+  if constexpr (RBW == 1) {
+    if (a.KT == 128 && a.M <= 6) return launch_staged<8, RBW, EPI, 16, false>(a, a.M, stream);
+    if (a.KT == 304 && a.M <= 3) return launch_staged<16, RBW, EPI, 19, false>(a, (76 * a.M + 63) / 64, stream);
+  }
   if (a.KT == 80 && a.M <= 8) {
     if constexpr (RBW == 1) return launch_half_cfg<8, RBW, EPI, 5>(a, stream);
     if constexpr (RBW == 2) return launch_half_cfg<4, RBW, EPI, 10>(a, stream);
