@@ -560,7 +560,7 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 
 // lm_head scores for RBW row-blocks (vocab rows) + the workgroup's argmax.
 // Grid: (NB / RBW) workgroups; partial[m * P + blockIdx.x] = best (score, index).
-template <int NW, int RBW, int U>
+template <int NW, int RBW, int U, int NC = 0>
 __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, float* __restrict__ logits,
     int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, int M, int KT) {
@@ -578,9 +578,15 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
   for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
-  accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
-
-  if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
+  if constexpr (NC > 0) {  // activations staged through LDS, NC chunks per lane
+    (void)xrow;
+    (void)ke;
+    accumulate_rows_staged<NW, RBW, U, NC, false>(acc, wt, x, ldx, M, KT, kb, wave, lane);
+    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RBW))) return;
+  } else {
+    accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
+    if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
+  }
 
   // Scan this lane's rows in increasing index order: strict '>' keeps the
   // lowest index among equal scores, the torch.argmax convention.
@@ -957,7 +963,34 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
   const int NB = V / kTileRows;
   const int KT = K / kTileK;
   const int P = NB / kLmHeadRBW;
-  if (KT == 80) {
+  auto staged = [&](auto tag) {
+    constexpr int kNC = decltype(tag)::value;
+    const size_t lds = (size_t)kLmHeadWaves * staged_wave_bytes(10, M, kLmHeadRBW);
+    lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC><<<dim3(P), dim3(kLmHeadWaves * 64), lds, stream>>>(
+        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+        KT);
+  };
+  // K/32 = 80: 8 waves x 10 k-tiles; for M <= 8 the activations are staged
+  // through LDS (the wave's 40 M chunks over 64 lanes).
+  if (KT == 80 && M <= 8) {
+    switch ((40 * M + 63) / 64) {
+      case 1:
+        staged(std::integral_constant<int, 1>{});
+        break;
+      case 2:
+        staged(std::integral_constant<int, 2>{});
+        break;
+      case 3:
+        staged(std::integral_constant<int, 3>{});
+        break;
+      case 4:
+        staged(std::integral_constant<int, 4>{});
+        break;
+      default:
+        staged(std::integral_constant<int, 5>{});
+        break;
+    }
+  } else if (KT == 80) {
     lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
         static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
         KT);
