@@ -311,7 +311,7 @@ def main() -> int:
     else:
         # Dominant kernel of the launch graph: the fused gate_up + SiLU*up
         # decode kernel (49% of the step's bytes), timed over 36 launches.
-        roof_kernel = "decode_half_kernel<4,2,1,10,0> (gate_up 19456x2560 + silu*up, M=1)"
+        roof_kernel = "decode_half_kernel<4,2,1,10,-3> (gate_up 19456x2560 + silu*up, M=1)"
         roof_bytes = G.projection_bytes("gate_up_proj", 1)
         achieved = roof_bytes / (per_kernel["gate_up_proj"]["us_per_launch"] * 1e-6) / 1e9
 
