@@ -189,6 +189,22 @@ class DecodeStep:
             raise ValueError(f"pos={pos} outside 0..{self.k_cache.shape[2] - 1}")
         self.pos_dev.fill_(pos)
 
+    def launch_next(self, embedding: torch.Tensor, tokens_out: torch.Tensor | None = None) -> None:
+        """One greedy decode step with no host work, for a graph captured once
+        and replayed per token (the loop of qwen_explicit_runtime_loop.py:
+        339-352 without its per-token dispatch): the embedding row of
+        self.token becomes the input, the token at position self.pos_dev is
+        computed (tokens_out[pos] = the new token, when given), and the
+        position advances by one.  embedding: [V, H] bf16 (the tied lm_head's
+        row-major copy serves)."""
+        if embedding.dim() != 2 or embedding.shape[1] != self.g.hidden_size or embedding.dtype != torch.bfloat16:
+            raise ValueError(f"embedding must be a bfloat16 [V, {self.g.hidden_size}] tensor")
+        torch.index_select(embedding, 0, self.token, out=self.hidden[0])
+        self.launch()
+        if tokens_out is not None:
+            tokens_out.index_copy_(0, self.pos_dev.long(), self.token)
+        self.pos_dev.add_(1)
+
     def launch(self, pos: int | None = None) -> None:
         """Enqueue the token at position `pos` (rows 0..pos-1 of every layer's
         cache are the context), or, with pos None, at the position in

@@ -348,3 +348,50 @@ def test_decode_step_one_graph_for_every_position(gpu):
     assert _same_bits(eager.k_cache, graphed.k_cache) and _same_bits(eager.v_cache, graphed.v_cache)
     with pytest.raises(ValueError):
         graphed.set_position(s_max)
+
+
+def test_decode_step_greedy_loop_in_one_graph(gpu):
+    """DecodeStep.launch_next captured once: four replays generate the same
+    tokens, caches and positions as four eager steps driven from the host
+    (embedding lookup, launch(pos), token read back)."""
+    from leanstack_amd.stack import DecodeStep, LayerProjections
+
+    n_layers, s_max, start = 2, 64, 7
+    layers_cpu, layers = [], []
+    for l in range(n_layers):
+        w, layer = _layer(9800 + 10 * l)
+        layers_cpu.append(w)
+        layers.append(LayerProjections(layer.attention.qkv_proj_weight, layer.attention.o_proj_weight,
+                                       layer.mlp.gate_up_proj_weight, layer.mlp.down_proj_weight))
+    norms = torch.stack([torch.stack((w["in_ln"], w["post_ln"])) for w in layers_cpu]).to(DEV)
+    qk = torch.stack([torch.stack((w["qn"], w["kn"])) for w in layers_cpu]).to(DEV)
+    gen = torch.Generator().manual_seed(9899)
+    final = (1 + 0.1 * torch.randn(G.hidden_size, generator=gen)).to(torch.bfloat16).to(DEV)
+    emb = weight(G.vocab_size, G.hidden_size, seed=9897).to(DEV)  # untied, so the tokens change
+    lm = PackedWeight.from_rowmajor(weight(G.vocab_size, G.hidden_size, seed=9898).to(DEV))
+    kc = torch.randn((n_layers, G.num_key_value_heads, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    vc = torch.randn((n_layers, G.num_key_value_heads, s_max, D), generator=gen).to(torch.bfloat16).to(DEV)
+    first = 1234
+
+    eager = DecodeStep(layers, norms, qk, final, lm, G, kc.clone(), vc.clone(), DEV)
+    token, expect = first, []
+    for pos in range(start, start + 4):
+        eager.hidden[0, 0] = emb[token]
+        eager.launch(pos)
+        token = eager.token.item()
+        expect.append(token)
+
+    looped = DecodeStep(layers, norms, qk, final, lm, G, kc.clone(), vc.clone(), DEV)
+    tokens = torch.full((s_max,), -1, dtype=torch.long, device=DEV)
+    looped.token.fill_(first)
+    looped.set_position(start)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        looped.launch_next(emb, tokens)
+    for _ in range(4):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert tokens[start:start + 4].tolist() == expect, (tokens[start:start + 4].tolist(), expect)
+    assert int(looped.pos_dev.item()) == start + 4
+    assert _same_bits(eager.k_cache, looped.k_cache) and _same_bits(eager.v_cache, looped.v_cache)
+    assert expect != [first] * 4  # the loop moved on from its first token
