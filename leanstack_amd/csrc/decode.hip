@@ -502,6 +502,22 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 #pragma unroll
   for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // Residual values of the outputs wave 0 will write, read before the
+  // weight stream so that their latency is not paid after the cross-wave
+  // sum (rows past M read row 0: in bounds, never stored).
+  float res[RBW][4];
+  if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd)) {
+    if (wave == 0) {
+#pragma unroll
+      for (int r = 0; r < RBW; ++r) {
+        const __bf16* rp = residual + (size_t)(m_active ? m : 0) * ldr + (rb0 + r) * 16 + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) res[r][i] = bf16_to_f32(rp[i]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
   static_assert(NORM <= 0 || U > 0, "the dense RMSNorm prologue is single-round");
@@ -548,8 +564,7 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float v = bf16_round(acc[r][i]);
-        if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd))
-          v = bf16_to_f32(residual[(size_t)m * ldr + n + i]) + v;
+        if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd)) v = res[r][i] + v;
         o[i] = bf16_bits(v);
       }
       *reinterpret_cast<u32x2_t*>(y + (size_t)m * ldy + n) =
