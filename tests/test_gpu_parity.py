@@ -51,8 +51,11 @@ def test_o_proj_gemv_config1(gpu):
 
 
 @pytest.mark.parametrize("name", sorted(PROJ))
-@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 def test_decode_projection(gpu, name, m):
+    """Every M of the decode forms: the staged-activation kernels switch their
+    chunks per lane with M (QKV 1..5 up to M = 8, o_proj 1..6 up to M = 6,
+    down 2..4 up to M = 3), then fragment loads per tile."""
     n, k = PROJ[name]
     w = weight(n, k, seed=10 + m)
     x = activations(m, k, seed=100 + m)
@@ -61,7 +64,7 @@ def test_decode_projection(gpu, name, m):
     assert_parity(y, expect, f"{name} M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8])
 def test_decode_gate_up_silu(gpu, m):
     n, k = 2 * G.intermediate_size, G.hidden_size
     w = weight(n, k, seed=20 + m)
@@ -71,7 +74,7 @@ def test_decode_gate_up_silu(gpu, m):
     assert_parity(y, expect, f"gate_up+silu M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_decode_down_residual(gpu, m):
     n, k = G.hidden_size, G.intermediate_size
     w = weight(n, k, seed=30 + m)
@@ -79,6 +82,17 @@ def test_decode_down_residual(gpu, m):
     r = activations(m, n, seed=301 + m)
     y = _gpu_linear(x, w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r)
     assert_parity(y, r + ref.linear(x, w), f"down+residual M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 5, 6])
+def test_decode_o_residual(gpu, m):
+    """o_proj with the residual epilogue (values read before the weight stream)."""
+    n, k = G.hidden_size, G.q_dim
+    w = weight(n, k, seed=40 + m)
+    x = activations(m, k, seed=400 + m)
+    r = activations(m, n, seed=401 + m)
+    y = _gpu_linear(x, w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r)
+    assert_parity(y, r + ref.linear(x, w), f"o+residual M={m}")
 
 
 @pytest.mark.parametrize("name", sorted(PROJ))
@@ -110,7 +124,7 @@ def test_prefill_residual(gpu):
     assert_parity(y, r + ref.linear(x, w), "o_proj+residual prefill")
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9])
 def test_lm_head_argmax_fp32(gpu, m):
     """Tied lm_head E[151936, 2560]: GPU argmax == CPU fp32-score argmax."""
     e = weight(G.vocab_size, G.hidden_size, seed=70)
@@ -123,7 +137,12 @@ def test_lm_head_argmax_fp32(gpu, m):
     expect = scores.argmax(dim=-1)
     margin = ref.top2_margin(scores)
     print(f"M={m} idx={idx.tolist()} margin={margin.tolist()}")
-    assert torch.equal(idx, expect)
+    top2 = scores.topk(2, dim=-1).indices
+    for row in range(m):
+        if margin[row] > 1e-3:  # a clear winner: the same index
+            assert idx[row] == expect[row], f"row {row}"
+        else:  # a near tie (fp32 summation order decides): one of the two
+            assert idx[row] in top2[row].tolist(), f"row {row}"
     assert_parity(logits.cpu(), scores, "lm_head fp32 logits")
 
 
