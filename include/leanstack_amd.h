@@ -219,6 +219,19 @@ int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K,
                             long long* out_idx,
                             void* workspace, size_t ws_bytes, void* hip_stream);
 
+/* The same with the final RMSNorm of x applied in the kernel (norm_weight
+ * [K] bf16, 16-byte aligned; eps): out_idx = argmax(rms_norm(x) . E^T), with
+ * each normalised value bf16(x*w*r) as in lsk_rmsnorm_linear_bf16.  K must
+ * be 2560 (the Qwen3-4B hidden size) and M at most 8.  Replaces the final
+ * norm and head of src/leanstack/runtime/qwen_explicit.py:952-960 (and,
+ * with LSK_LOGITS_FP32, the norm in front of cutile_logits_argmax,
+ * qwen_explicit.py:1807-1832) in one launch plus the argmax stage. */
+int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K,
+                                    const void* x, int M, int ldx,
+                                    const void* norm_weight, float eps,
+                                    float* logits_opt, int logits_mode, long long* out_idx,
+                                    void* workspace, size_t ws_bytes, void* hip_stream);
+
 /* ------------------------------------------------------------------------
  * Stack programs: a whole decode / verify step of projections in ONE launch.
  *

@@ -311,10 +311,12 @@ int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_di
   return LSK_OK;
 }
 
-int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
-                            float* logits_opt, int logits_mode, long long* out_idx, void* workspace,
-                            size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
+namespace {
+
+// Checks and launch shared by the plain and the RMSNorm lm_head entry points.
+int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                   const void* norm_weight, float eps, float* logits_opt, int logits_mode, long long* out_idx,
+                   void* workspace, size_t ws_bytes, void* hip_stream) {
   if (layout_id != LSK_LAYOUT_MFMA16X32)
     return fail(LSK_ERR_LAYOUT, "lm_head needs layout %d, got %d", LSK_LAYOUT_MFMA16X32, layout_id);
   if (int st = check_shape(layout_id, V, K)) return st;
@@ -334,10 +336,34 @@ int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, c
   if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 8))
     return fail(LSK_ERR_WORKSPACE, "lm_head workspace needs %zu bytes, got %zu", need, workspace ? ws_bytes : 0);
   hipError_t err = lsk::launch_lm_head_argmax(w_packed, V, K, x, M, ldx, logits_opt, logits_mode == LSK_LOGITS_BF16,
-                                              out_idx, static_cast<lsk::ArgmaxPartial*>(workspace),
+                                              out_idx, static_cast<lsk::ArgmaxPartial*>(workspace), norm_weight, eps,
                                               static_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess) return hip_fail(err, "lm_head kernel launch");
   return LSK_OK;
+}
+
+}  // namespace
+
+int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                            float* logits_opt, int logits_mode, long long* out_idx, void* workspace,
+                            size_t ws_bytes, void* hip_stream) {
+  g_last_error.clear();
+  return lm_head_argmax(w_packed, layout_id, V, K, x, M, ldx, nullptr, 0.f, logits_opt, logits_mode, out_idx,
+                        workspace, ws_bytes, hip_stream);
+}
+
+int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                                    const void* norm_weight, float eps, float* logits_opt, int logits_mode,
+                                    long long* out_idx, void* workspace, size_t ws_bytes, void* hip_stream) {
+  g_last_error.clear();
+  if (K != 80 * lsk::kTileK || M > 8)
+    return fail(LSK_ERR_INVALID, "the RMSNorm lm_head serves K=%d and M <= 8 (got K=%d, M=%d)", 80 * lsk::kTileK, K,
+                M);
+  if (norm_weight == nullptr || !aligned(norm_weight, 16))
+    return fail(LSK_ERR_INVALID, "the norm weight must be a 16-byte aligned device pointer");
+  if (!std::isfinite(eps) || eps < 0.f) return fail(LSK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
+  return lm_head_argmax(w_packed, layout_id, V, K, x, M, ldx, norm_weight, eps, logits_opt, logits_mode, out_idx,
+                        workspace, ws_bytes, hip_stream);
 }
 
 }  // extern "C"

@@ -575,10 +575,14 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
 
 // lm_head scores for RBW row-blocks (vocab rows) + the workgroup's argmax.
 // Grid: (NB / RBW) workgroups; partial[m * P + blockIdx.x] = best (score, index).
-template <int NW, int RBW, int U, int NC = 0>
+// NC > 0: the activations staged through LDS (NC chunks per lane), or with
+// NORM their RMSNorm (norm_w, eps) applied on the way (the dense prologue).
+template <int NW, int RBW, int U, int NC = 0, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, float* __restrict__ logits,
-    int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, int M, int KT) {
+    int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, int M, int KT,
+    const __bf16* __restrict__ norm_w, float eps) {
+  static_assert(!NORM || NC > 0, "the RMSNorm prologue is the dense single-round one");
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m = lane & 15;
@@ -593,12 +597,22 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
   for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
-  if constexpr (NC > 0) {  // activations staged through LDS, NC chunks per lane
+  if constexpr (NORM) {
     (void)xrow;
     (void)ke;
+    accumulate_rows_rms_dense<NW, RBW, U, NC>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w), M, KT,
+                                              kb, wave, lane, eps);
+    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NC, M, RBW))) return;
+  } else if constexpr (NC > 0) {  // activations staged through LDS, NC chunks per lane
+    (void)xrow;
+    (void)ke;
+    (void)norm_w;
+    (void)eps;
     accumulate_rows_staged<NW, RBW, U, NC, false>(acc, wt, x, ldx, M, KT, kb, wave, lane);
     if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RBW))) return;
   } else {
+    (void)norm_w;
+    (void)eps;
     accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
     if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
   }
@@ -974,16 +988,24 @@ int lm_head_partials(int V) { return (V / kTileRows) / kLmHeadRBW; }
 
 hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int M, int ldx, float* logits,
                                  int logits_bf16, long long* out_idx, ArgmaxPartial* partials,
-                                 hipStream_t stream) {
+                                 const void* norm_w, float eps, hipStream_t stream) {
   const int NB = V / kTileRows;
   const int KT = K / kTileK;
   const int P = NB / kLmHeadRBW;
+  const auto* nw = static_cast<const __bf16*>(norm_w);
   auto staged = [&](auto tag) {
     constexpr int kNC = decltype(tag)::value;
-    const size_t lds = (size_t)kLmHeadWaves * staged_wave_bytes(10, M, kLmHeadRBW);
-    lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC><<<dim3(P), dim3(kLmHeadWaves * 64), lds, stream>>>(
-        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
-        KT);
+    if (nw != nullptr) {
+      const size_t lds = (size_t)kLmHeadWaves * rms_wave_bytes(10, kNC, M, kLmHeadRBW);
+      lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC, true><<<dim3(P), dim3(kLmHeadWaves * 64), lds, stream>>>(
+          static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+          KT, nw, eps);
+    } else {
+      const size_t lds = (size_t)kLmHeadWaves * staged_wave_bytes(10, M, kLmHeadRBW);
+      lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC><<<dim3(P), dim3(kLmHeadWaves * 64), lds, stream>>>(
+          static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+          KT, nullptr, 0.f);
+    }
   };
   // K/32 = 80: 8 waves x 10 k-tiles; for M <= 8 the activations are staged
   // through LDS (the wave's 40 M chunks over 64 lanes).
@@ -1005,14 +1027,16 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
         staged(std::integral_constant<int, 5>{});
         break;
     }
+  } else if (nw != nullptr) {
+    return hipErrorInvalidValue;  // the fused RMSNorm serves K = 2560, M <= 8 (checked by the caller)
   } else if (KT == 80) {
     lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
         static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
-        KT);
+        KT, nullptr, 0.f);
   } else {
     lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 0><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
         static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
-        KT);
+        KT, nullptr, 0.f);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;

@@ -145,7 +145,7 @@ int lm_head_partials(int V);
 
 hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int M, int ldx,
                                  float* logits, int logits_bf16, long long* out_idx,
-                                 ArgmaxPartial* partials, hipStream_t stream);
+                                 ArgmaxPartial* partials, const void* norm_w, float eps, hipStream_t stream);
 
 // Workspace bytes the split-K prefill path needs on `device` for this shape
 // (0 when the shape does not take it).  Sets *status to a HIP error if the

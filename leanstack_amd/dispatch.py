@@ -295,16 +295,32 @@ def _greedy_rows(hidden: torch.Tensor, lm_head_weight: PackedWeight, logits_mode
     return kernels.lm_head_argmax(hidden.reshape(-1, w.k), w, logits_mode=logits_mode)
 
 
+def _greedy_rows_normed(rows: torch.Tensor, final_norm_weight, lm_head_weight, rms_norm_eps,
+                        logits_mode: int) -> torch.Tensor:
+    """Final RMSNorm + head + argmax of [M, H] rows: in the lm_head kernel
+    (lsk_rmsnorm_lm_head_argmax_bf16) for the Qwen3-4B hidden size and up to
+    8 rows, else a separate norm in front of the head."""
+    w = _require_packed(lm_head_weight, "lm_head_weight")
+    rows = rows.reshape(-1, w.k)
+    if w.k == 2560 and rows.shape[0] <= 8 and final_norm_weight.dtype == torch.bfloat16 and \
+            final_norm_weight.device.type == "cuda":
+        return kernels.lm_head_argmax(rows, w, logits_mode=logits_mode, norm_weight=final_norm_weight,
+                                      eps=rms_norm_eps)
+    normed = torch.nn.functional.rms_norm(rows, (w.k,), final_norm_weight, rms_norm_eps)
+    return _greedy_rows(normed, w, logits_mode)
+
+
 def _semantic_greedy_head_vector(hidden_states, final_norm_weight, lm_head_weight, rms_norm_eps):
-    """RMSNorm, bf16 logits, first maximum -> int64 [1, 1] (qwen_explicit.py:952-960)."""
-    normed = qwen_rmsnorm_vector(hidden_states, final_norm_weight, rms_norm_eps)
-    return _greedy_rows(normed, lm_head_weight, _lib.LOGITS_BF16).view(1, 1)
+    """RMSNorm, bf16 logits, first maximum -> int64 [1, 1] (qwen_explicit.py:952-960),
+    the norm inside the lm_head kernel."""
+    return _greedy_rows_normed(hidden_states, final_norm_weight, lm_head_weight, rms_norm_eps,
+                               _lib.LOGITS_BF16).view(1, 1)
 
 
 def _semantic_greedy_head(hidden_states, final_norm_weight, lm_head_weight, rms_norm_eps):
     """RMSNorm, bf16 logits of the last position, argmax -> [B, 1] (qwen_explicit.py:916-929)."""
-    normed = qwen_rmsnorm(hidden_states, final_norm_weight, rms_norm_eps)
-    return _greedy_rows(normed[:, -1, :], lm_head_weight, _lib.LOGITS_BF16).view(-1, 1)
+    return _greedy_rows_normed(hidden_states[:, -1, :], final_norm_weight, lm_head_weight, rms_norm_eps,
+                               _lib.LOGITS_BF16).view(-1, 1)
 
 
 def hip_logits_argmax(hidden_states: torch.Tensor, lm_head_weight: PackedWeight, *, vocab_tile: int = 128,
@@ -351,8 +367,8 @@ def select_semantic_greedy_token(runtime, hidden_states: torch.Tensor) -> torch.
     last = last_hidden_vector(hidden_states)
     backend = resolve_semantic_logits_backend()
     if backend in {"auto", "cutile", "hip"}:
-        normed = qwen_rmsnorm_vector(last, runtime.final_norm_weight, runtime.config.rms_norm_eps)
-        return hip_logits_argmax(normed, runtime.lm_head_weight)
+        return _greedy_rows_normed(last, runtime.final_norm_weight, runtime.lm_head_weight,
+                                   runtime.config.rms_norm_eps, _lib.LOGITS_FP32).view(1, 1)
     return _semantic_greedy_head_vector(last, runtime.final_norm_weight, runtime.lm_head_weight,
                                         runtime.config.rms_norm_eps)
 

@@ -254,11 +254,14 @@ class LmHeadWorkspace:
 
 def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: int = _lib.LOGITS_FP32,
                    logits_out: torch.Tensor | None = None, workspace: LmHeadWorkspace | None = None,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None,
+                   eps: float = 1e-6) -> torch.Tensor:
     """Greedy token per row: int64 [M] = argmax over the vocab of hidden . W^T.
 
     logits_mode LOGITS_FP32 compares fp32 scores (cuTile head); LOGITS_BF16
-    compares bf16-rounded logits (torch.mv head).  Lowest index wins ties."""
+    compares bf16-rounded logits (torch.mv head).  Lowest index wins ties.
+    norm_weight: the final RMSNorm ([K] bf16, with eps) applied to hidden in
+    the kernel (K = 2560, M <= 8)."""
     if not isinstance(weight, PackedWeight) or weight.layout != _lib.LAYOUT_MFMA16X32:
         raise ValueError("lm_head weight must be a PackedWeight in the mfma16x32 layout")
     lib = _lib.load()
@@ -274,6 +277,18 @@ def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: i
         if logits_out.dtype != torch.float32 or logits_out.numel() != m * v or not logits_out.is_contiguous():
             raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{v}")
         logits_ptr = logits_out.data_ptr()
+    if norm_weight is not None:
+        _require_device(norm_weight, "norm_weight")
+        if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != weight.k:
+            raise ValueError(f"norm_weight must be a bfloat16 tensor of {weight.k} values")
+        nw = norm_weight.reshape(-1).contiguous()
+        status = lib.lsk_rmsnorm_lm_head_argmax_bf16(
+            weight.data.data_ptr(), weight.layout, v, weight.k, h2.data_ptr(), m, ldx, nw.data_ptr(), float(eps),
+            logits_ptr, logits_mode, out.data_ptr(), workspace.buffer.data_ptr(), workspace.buffer.numel(),
+            stream_handle(),
+        )
+        _lib.check(status, "lsk_rmsnorm_lm_head_argmax_bf16")
+        return out
     status = lib.lsk_lm_head_argmax_bf16(
         weight.data.data_ptr(), weight.layout, v, weight.k,
         h2.data_ptr(), m, ldx,

@@ -174,7 +174,6 @@ class DecodeStep:
         self.qkv = torch.empty((1, g.qkv_dim), device=device, dtype=torch.bfloat16)
         self.attn = torch.empty((g.q_dim,), device=device, dtype=torch.bfloat16)
         self.act = torch.empty((1, g.intermediate_size), device=device, dtype=torch.bfloat16)
-        self.normed = torch.empty((1, h), device=device, dtype=torch.bfloat16)
         self.head_ws = kernels.LmHeadWorkspace(1, lm_head.n, lm_head.k, device)
         ws_bytes = _lib.load().lsk_attention_workspace_bytes(g.num_attention_heads, g.num_key_value_heads,
                                                                g.head_dim, max_seq)
@@ -228,7 +227,6 @@ class DecodeStep:
                                    out=self.act)
             kernels.linear(self.act, p.down, epilogue=_lib.EPI_RESIDUAL_ADD, residual=self.mid, out=y)
         last = self.hidden[len(self.layers) % 2]
-        # the final norm stays torch (qwen_explicit.py:952-960): one norm per token
-        self.normed.copy_(torch.nn.functional.rms_norm(last, (g.hidden_size,), self.final_norm, self.eps))
-        kernels.lm_head_argmax(self.normed, self.lm_head, logits_mode=_lib.LOGITS_BF16, workspace=self.head_ws,
-                               out=self.token)
+        # final RMSNorm + bf16 logits + argmax (qwen_explicit.py:952-960) in the lm_head kernel
+        kernels.lm_head_argmax(last, self.lm_head, logits_mode=_lib.LOGITS_BF16, workspace=self.head_ws,
+                               out=self.token, norm_weight=self.final_norm, eps=self.eps)

@@ -169,6 +169,26 @@ def test_lm_head_rejects_before_launch():
         assert st == code, (over, _lib.last_error())
 
 
+def test_rmsnorm_lm_head_rejects_before_launch():
+    lib = _lib.load()
+    ws = lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 8, 151936, 2560)
+    cases = [
+        (dict(K=4096), _lib.ERR_INVALID),       # the fused norm serves K = 2560
+        (dict(M=9), _lib.ERR_INVALID),          # and up to 8 rows
+        (dict(nw=0), _lib.ERR_INVALID),         # no norm weight
+        (dict(nw=FAKE + 8), _lib.ERR_INVALID),  # misaligned norm weight
+        (dict(eps=-1.0), _lib.ERR_INVALID),
+        (dict(layout=2), _lib.ERR_LAYOUT),
+        (dict(ws=8), _lib.ERR_WORKSPACE),
+    ]
+    for over, code in cases:
+        a = dict(V=151936, K=2560, M=1, nw=FAKE, eps=1e-6, layout=1, ws=ws)
+        a.update(over)
+        st = lib.lsk_rmsnorm_lm_head_argmax_bf16(FAKE, a["layout"], a["V"], a["K"], FAKE, a["M"], a["K"],
+                                                 a["nw"] or None, a["eps"], None, 0, FAKE, FAKE, a["ws"], None)
+        assert st == code, (over, _lib.last_error())
+
+
 def test_stack_prepare_rejects_bad_programs():
     lib = _lib.load()
     good = _lib.Projection(FAKE, 1, 6144, 2560, FAKE, 2560, FAKE, 6144, 0, None, 0, -1)

@@ -146,6 +146,30 @@ def test_lm_head_argmax_fp32(gpu, m):
     assert_parity(logits.cpu(), scores, "lm_head fp32 logits")
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+def test_rmsnorm_lm_head_argmax(gpu, m):
+    """The final RMSNorm inside the lm_head kernel: argmax of
+    rms_norm(h) . E^T against the oracle's norm and fp32 scores (a near tie
+    may go either way), logits at the parity bar."""
+    e = weight(G.vocab_size, G.hidden_size, seed=71)
+    h = activations(m, G.hidden_size, seed=710 + m) * 3
+    gen = torch.Generator().manual_seed(720 + m)
+    nw = (1 + 0.2 * torch.randn(G.hidden_size, generator=gen)).to(torch.bfloat16)
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(e.to(dev))
+    logits = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
+    idx = kernels.lm_head_argmax(h.to(dev), pw, logits_out=logits, norm_weight=nw.to(dev), eps=1e-6).cpu()
+    scores = ref.logits_scores_fp32(ref.rmsnorm(h, nw, 1e-6), e)
+    margin = ref.top2_margin(scores)
+    top2 = scores.topk(2, dim=-1).indices
+    for row in range(m):
+        if margin[row] > 1e-2:
+            assert idx[row] == scores[row].argmax(), f"row {row}"
+        else:
+            assert idx[row] in top2[row].tolist(), f"row {row}"
+    assert_parity(logits.cpu(), scores, f"rmsnorm lm_head M={m} logits")
+
+
 def test_lm_head_argmax_bf16_mode(gpu):
     """bf16-rounded logits: matches torch.mv(W, h).argmax (first maximum)."""
     e = weight(G.vocab_size, G.hidden_size, seed=71)
