@@ -727,6 +727,18 @@ template <int NW, int RBW, int EPI, int U, int NORM>
 hipError_t launch_decode_cfg(const DecodeArgs& a, hipStream_t stream) {
   auto* kernel = decode_linear_kernel<NW, RBW, EPI, U, NORM>;
   size_t lds = NORM < -1 ? (size_t)NW * staged_wave_bytes(U, a.M, RBW) : 0;
+  if constexpr (NORM < -1) {
+    if (lds > kDefaultDynamicLds) {
+      // Raised once per kernel, to what M = 8 (the largest staged M) needs.
+      static std::once_flag once;
+      static hipError_t raised = hipSuccess;
+      std::call_once(once, [&] {
+        raised = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     NW * staged_wave_bytes(U, 8, RBW));
+      });
+      if (raised != hipSuccess) return raised;
+    }
+  }
   if constexpr (NORM > 0) {
     lds = (size_t)NW * rms_wave_bytes(U, NORM, a.M, RBW);
     if (lds > kDefaultDynamicLds) {
@@ -855,7 +867,7 @@ hipError_t launch_half_cfg(const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// The staged-activation form with NC (1..6) chunks per lane; HALF selects
+// The staged-activation form with NC (1..8) chunks per lane; HALF selects
 // decode_half_kernel (U = pairs per wave), else decode_linear_kernel.
 template <int NW, int RBW, int EPI, int U, bool HALF>
 hipError_t launch_staged(const DecodeArgs& a, int nc, hipStream_t stream) {
@@ -877,6 +889,10 @@ hipError_t launch_staged(const DecodeArgs& a, int nc, hipStream_t stream) {
       return go(std::integral_constant<int, 5>{});
     case 6:
       return go(std::integral_constant<int, 6>{});
+    case 7:
+      return go(std::integral_constant<int, 7>{});
+    case 8:
+      return go(std::integral_constant<int, 8>{});
     default:
       return hipErrorInvalidValue;
   }
@@ -894,9 +910,9 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
   // (160 row-blocks) measured slower as halves: 320 workgroups leave 64 CUs
   // with two.
   // Activations staged through LDS (staged_x(NC), NC = chunks per lane of
-  // the wave's M * 4 * k-tiles chunks) wherever the registers and 64 KB of
-  // LDS allow: QKV for every M <= 8, gate_up (4 waves x 10 pairs up to
-  // M = 2, then 8 waves x 5), o_proj up to M = 6, down up to M = 3.
+  // the wave's M * 4 * k-tiles chunks) wherever the registers allow: QKV and
+  // o_proj for every M <= 8, gate_up (4 waves x 10 pairs up to M = 2, then
+  // 8 waves x 5), down up to M = 6 (its 16 waves then hold 118 KB of LDS).
   if (a.KT == 80 && a.M <= 8) {
     if constexpr (RBW == 1) return launch_staged<8, RBW, EPI, 5, true>(a, (40 * a.M + 63) / 64, stream);
     if constexpr (RBW == 2) {
@@ -905,8 +921,8 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
     }
   }
   if constexpr (RBW == 1) {
-    if (a.KT == 128 && a.M <= 6) return launch_staged<8, RBW, EPI, 16, false>(a, a.M, stream);
-    if (a.KT == 304 && a.M <= 3) return launch_staged<16, RBW, EPI, 19, false>(a, (76 * a.M + 63) / 64, stream);
+    if (a.KT == 128 && a.M <= 8) return launch_staged<8, RBW, EPI, 16, false>(a, a.M, stream);
+    if (a.KT == 304 && a.M <= 6) return launch_staged<16, RBW, EPI, 19, false>(a, (76 * a.M + 63) / 64, stream);
   }
   if (a.KT == 80 && a.M <= 8) {
     if constexpr (RBW == 1) return launch_half_cfg<8, RBW, EPI, 5>(a, stream);
