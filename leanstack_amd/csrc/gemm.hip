@@ -807,7 +807,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   const int chunk = r / k.R;
   const int i = r % k.R;
   int nb, mb;
-  tile_coords(k.dp + i, g.n_blocks, g.m_blocks, nb, mb);
+  if (k.dp == 0 && k.R % 8 == 0 && g.m_blocks % 2 == 0) {
+    // Every block split (one partial round): workgroup r runs on XCD
+    // i % 8, so give XCD x the contiguous run [x R/8, (x+1) R/8) of an
+    // order grouped by token-block pairs; each XCD then covers a
+    // rectangle (e.g. 5 weight blocks x 2 token blocks at 2048 tokens)
+    // instead of every weight block of one token block.  down_proj at
+    // 2048 tokens: 139 -> 134 us.  The map i -> (nb, mb) is one to one.
+    const int i2 = (i % 8) * (k.R / 8) + i / 8;
+    const int group = i2 / (2 * g.n_blocks);
+    mb = group * 2 + i2 % 2;
+    nb = (i2 - group * 2 * g.n_blocks) / 2;
+  } else {
+    tile_coords(k.dp + i, g.n_blocks, g.m_blocks, nb, mb);
+  }
   const int u0 = chunk * k.units / k.S, u1 = (chunk + 1) * k.units / k.S;
   mainloop(acc, g, lds, nb, mb, 2 * u0, 2 * u1);
 
