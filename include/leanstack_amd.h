@@ -295,6 +295,15 @@ int lsk_stack_error(void* workspace, int* error_out);
  * library GEMMs have no cross-workgroup waits. */
 int lsk_linear_error(void* workspace, int* error_out);
 
+/* Polls of a split-K arrival word before a prefill workgroup stops waiting
+ * for the other chunks of its output block (default 4194304, about 0.1 s).
+ * A workgroup that gives up sets the workspace's error word (see
+ * lsk_linear_error) and writes NaN to its share of the block, so a lost wait
+ * is never returned as a result.  Applies to launches after the call; used
+ * by tests to force the give-up path from the host.  No counterpart in the
+ * reference, whose library GEMMs have no cross-workgroup waits. */
+void lsk_set_linear_wait_limit(unsigned polls);
+
 #ifdef __cplusplus
 }
 #endif

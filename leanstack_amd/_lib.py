@@ -110,6 +110,7 @@ _SIGNATURES.update({
     "lsk_stack_run": (_c_int, [_c_void, _c_int, _c_void, _c_size, _c_void]),
     "lsk_stack_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
     "lsk_linear_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
+    "lsk_set_linear_wait_limit": (None, [ctypes.c_uint]),
 })
 
 _lock = threading.Lock()

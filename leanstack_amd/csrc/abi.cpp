@@ -504,4 +504,6 @@ int lsk_linear_error(void* workspace, int* error_out) {
   return read_clear_error_word(workspace, 0, error_out);
 }
 
+void lsk_set_linear_wait_limit(unsigned polls) { lsk::set_linear_wait_limit(polls); }
+
 }  // extern "C"

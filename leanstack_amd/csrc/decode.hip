@@ -573,6 +573,25 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
   }
 }
 
+// The order torch.argmax reduces in: NaN above every number (the first NaN
+// wins), then the larger value, then the lower index among equal values.  An
+// all -inf row therefore yields its first index, never the INT_MAX of an
+// empty candidate, so the token id is always a valid vocab row.
+__device__ __forceinline__ bool argmax_beats(float s, int i, float best, int best_idx) {
+  const bool s_nan = s != s;
+  const bool b_nan = best != best;
+  if (s_nan != b_nan) return s_nan;
+  if (!s_nan && s != best) return s > best;
+  return i < best_idx;
+}
+
+__device__ __forceinline__ void argmax_take(float& best, int& best_idx, float s, int i) {
+  if (argmax_beats(s, i, best, best_idx)) {
+    best = s;
+    best_idx = i;
+  }
+}
+
 // lm_head scores for RBW row-blocks (vocab rows) + the workgroup's argmax.
 // Grid: (NB / RBW) workgroups; partial[m * P + blockIdx.x] = best (score, index).
 // NC > 0: the activations staged through LDS (NC chunks per lane), or with
@@ -617,8 +636,8 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
   }
 
-  // Scan this lane's rows in increasing index order: strict '>' keeps the
-  // lowest index among equal scores, the torch.argmax convention.
+  // Scan this lane's rows in increasing index order with the torch.argmax
+  // order (argmax_beats): every row, -inf and NaN included, gets a real index.
   float best = -__builtin_huge_valf();
   int best_idx = INT_MAX;
 #pragma unroll
@@ -631,22 +650,14 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     }
     if (logits != nullptr && m_active) *reinterpret_cast<f32x4_t*>(logits + (size_t)m * V + n0) = s;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (s[i] > best) {
-        best = s[i];
-        best_idx = n0 + i;
-      }
-    }
+    for (int i = 0; i < 4; ++i) argmax_take(best, best_idx, s[i], n0 + i);
   }
   // Lanes m, m+16, m+32, m+48 hold the same column: combine them.
 #pragma unroll
   for (int off = 16; off <= 32; off <<= 1) {
     const float os = __shfl_xor(best, off);
     const int oi = __shfl_xor(best_idx, off);
-    if (os > best || (os == best && oi < best_idx)) {
-      best = os;
-      best_idx = oi;
-    }
+    argmax_take(best, best_idx, os, oi);
   }
   if (g == 0 && m_active) partial[(size_t)m * gridDim.x + blockIdx.x] = ArgmaxPartial{best, best_idx};
 }
@@ -659,12 +670,6 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
 constexpr int kFinalizeThreads = 1024;
 constexpr int kFinalizePerThread = 8;
 
-__device__ __forceinline__ void better_of(float& best, int& best_idx, float s, int i) {
-  if (s > best || (s == best && i < best_idx)) {
-    best = s;
-    best_idx = i;
-  }
-}
 
 __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const ArgmaxPartial* __restrict__ partial,
                                                                            int P, long long* __restrict__ out_idx) {
@@ -680,13 +685,13 @@ __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const
       c[j] = p < P ? row[p] : ArgmaxPartial{-__builtin_huge_valf(), INT_MAX};
     }
 #pragma unroll
-    for (int j = 0; j < kFinalizePerThread; ++j) better_of(best, best_idx, c[j].score, c[j].index);
+    for (int j = 0; j < kFinalizePerThread; ++j) argmax_take(best, best_idx, c[j].score, c[j].index);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float os = __shfl_xor(best, off);
     const int oi = __shfl_xor(best_idx, off);
-    better_of(best, best_idx, os, oi);
+    argmax_take(best, best_idx, os, oi);
   }
   constexpr int kW = kFinalizeThreads / 64;
   __shared__ float s_best[kW];
@@ -698,7 +703,7 @@ __global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kW; ++w) better_of(best, best_idx, s_best[w], s_idx[w]);
+    for (int w = 1; w < kW; ++w) argmax_take(best, best_idx, s_best[w], s_idx[w]);
     out_idx[m] = best_idx;
   }
 }

@@ -21,6 +21,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -28,6 +29,10 @@
 
 namespace lsk {
 namespace {
+
+// Polls of a split block's arrival word before a split-K wait gives up
+// (set_linear_wait_limit).
+std::atomic<unsigned> g_wait_limit{kSkSpinLimit};
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -747,8 +752,11 @@ __device__ __forceinline__ void zero(f32x16_t (&acc)[4][4]) {
 // [16s/S, 16(s+1)/S) of the block over the S slots in chunk order and
 // stores them with the epilogue, then counts itself out; the last one out
 // clears both words.  R*S <= G, and whole-K blocks never wait, so every
-// split workgroup gets a CU; the waits are bounded anyway (a workgroup that
-// gives up records it in the error word and stores what it has).  The order
+// split workgroup gets a CU.  That holds only while no other kernel shares
+// the device, so the waits are bounded: a workgroup that gives up (after
+// Split::spin_limit polls) records it in the error word and stores NaN for
+// its tiles instead of a partial sum, so a lost wait can never pass for a
+// result.  The order
 // of every sum is fixed by (T, G), so results are bitwise reproducible.
 // Partials cross XCDs, whose L2s are not coherent with each other, so they
 // are written and read with device-coherent (sc1) accesses, the ones
@@ -782,6 +790,7 @@ struct Split {
   int R;                    // blocks split
   int S;                    // chunks per split block (1 = no split)
   int units;                // 128-K units per block (KT / 4)
+  unsigned spin_limit;      // polls of the arrival word before a wait gives up
 };
 
 template <int EPI>
@@ -847,18 +856,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   __syncthreads();
   unsigned* arrive = k.flags + 2 * i;
   unsigned* depart = arrive + 1;
+  __shared__ int gave_up;
   if (tid == 0) {
+    gave_up = 0;
     __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned spins = 0;
     while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)k.S) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++spins > kSkSpinLimit) {
+      if (spins++ >= k.spin_limit) {
         __hip_atomic_store(k.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        gave_up = 1;
         break;
       }
+      __builtin_amdgcn_s_sleep(2);
     }
   }
   __syncthreads();
+  const bool poison = gave_up != 0;
 
   // Sum this workgroup's share of the block's tiles over the S chunks.
   const unsigned first = (unsigned)i * (unsigned)kSkPartialBytes;
@@ -877,6 +890,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
                                                kCoherent));
 #pragma unroll
       for (int q = 0; q < 4; ++q) sum[q] += v[q];
+    }
+    if (poison) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                                                   __builtin_nanf("")};
     }
     store_one_tile<EPI>([&](int p) { return make_float2(sum[p >> 1][2 * (p & 1)], sum[p >> 1][2 * (p & 1) + 1]); },
                         g, nb, mb, ab >> 2, ab & 3);
@@ -943,6 +961,7 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
   k.flags = ws != nullptr ? reinterpret_cast<unsigned*>(ws + kSkFlagsOffset) : nullptr;
   k.partials = ws != nullptr ? ws + kSkPartialsOffset : nullptr;
   k.partial_bytes = (unsigned)((size_t)k.R * k.S * kSkPartialBytes);
+  k.spin_limit = g_wait_limit.load(std::memory_order_relaxed);
   gemm_wdx_kernel<EPI><<<dim3(k.dp + k.R * k.S), dim3(kThreads), 0, stream>>>(g, k);
   return hipGetLastError();
 }
@@ -989,6 +1008,8 @@ hipError_t sk_grid(int device, int* grid_out) {
 }
 
 }  // namespace
+
+void set_linear_wait_limit(unsigned polls) { g_wait_limit.store(polls, std::memory_order_relaxed); }
 
 size_t gemm_workspace_bytes(int device, int M, int N, int K, hipError_t* status) {
   *status = hipSuccess;

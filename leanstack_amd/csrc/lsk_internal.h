@@ -152,6 +152,10 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
 // device query fails.
 size_t gemm_workspace_bytes(int device, int M, int N, int K, hipError_t* status);
 
+// Polls of a split-K arrival word before the wait gives up (default
+// kSkSpinLimit); applies to launches made after the call.
+void set_linear_wait_limit(unsigned polls);
+
 // Prefill GEMM launch (any M >= 1; used for M > kDecodeMaxM).  With a
 // workspace of at least gemm_workspace_bytes() the last partial round of
 // output blocks is split along K over the idle CUs;

@@ -39,23 +39,55 @@ def stream_handle() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-_prefill_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+def _check_out(out: torch.Tensor, m: int, n_out: int, dtype: torch.dtype, what: str = "out") -> None:
+    """A caller-supplied output must hold exactly the m x n_out values the
+    kernel writes, contiguously: the C layer sees only a pointer."""
+    if out.dtype != dtype or out.shape[-1:] != (n_out,) or out.numel() != m * n_out or not out.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous {dtype} tensor of {m} x {n_out} values "
+                         f"(got {out.dtype} {tuple(out.shape)})")
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _device_workspace(cache: dict[int, torch.Tensor], device: torch.device, nbytes: int, what: str) -> torch.Tensor:
+    """The zero-filled workspace of `cache` for `device`, grown to `nbytes`.
+    One per device: calls that share it must be stream-ordered (callers on
+    concurrent streams pass workspaces of their own).  It is never allocated
+    while the stream is being captured, so a captured graph never replays a
+    workspace's allocation or zero fill."""
+    key = _device_index(device)
+    ws = cache.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"the {what} workspace must be allocated before graph capture: run the same "
+                               f"launch once outside the capture first")
+        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+        cache[key] = ws
+    return ws
+
+
+_prefill_workspaces: dict[int, torch.Tensor] = {}
 
 
 def prefill_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor | None:
-    """The split-K workspace of the prefill GEMM for the current stream of
-    `device` (zero-filled once, left zero-filled by every call), or None when
-    the shape does not use one.  One per (device, stream), because calls that
-    share a workspace must be stream-ordered."""
+    """The split-K workspace of the prefill GEMM on `device` (zero-filled
+    once, left zero-filled by every call), or None when the shape does not
+    use one."""
     nbytes = _lib.load().lsk_workspace_bytes(_lib.OP_LINEAR, m, n, k)
     if nbytes == 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle() or 0)
-    ws = _prefill_workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
-        _prefill_workspaces[key] = ws
-    return ws
+    return _device_workspace(_prefill_workspaces, device, nbytes, "prefill")
+
+
+def set_linear_wait_limit(polls: int) -> None:
+    """Polls of a split-K arrival word before a prefill workgroup gives up
+    (then the workspace's error word is set and its tiles are NaN)."""
+    _lib.load().lsk_set_linear_wait_limit(int(polls))
+
+
+LINEAR_WAIT_LIMIT_DEFAULT = 1 << 22
 
 
 def linear_error(workspace: torch.Tensor) -> int:
@@ -73,28 +105,32 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
 
     epilogue EPI_NONE (N' = N), EPI_SILU_MUL (gate_up layout, N' = N/2,
     SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection).
-    workspace: "auto" uses the per-stream split-K workspace for prefill
-    shapes (prefill_workspace), None runs one workgroup per output block, a
-    uint8 device tensor is used as given."""
+    workspace: "auto" uses the device's split-K workspace for prefill shapes
+    (prefill_workspace; calls on concurrent streams pass their own), None
+    runs one workgroup per output block, a uint8 device tensor is used as
+    given.  A split-K workgroup whose bounded wait gives up (possible only
+    when another kernel holds CUs the split needs) sets the workspace's error
+    word (linear_error) and writes NaN to its tiles."""
     if not isinstance(weight, PackedWeight):
         raise ValueError("weight must be a PackedWeight (pack it with leanstack_amd.layout / leanserve)")
     lib = _lib.load()
-    _require_device(x, "x")
-    _require_device(weight.data, "weight")
     x2, m, ldx = _rows(x, weight.k, "x")
     n_out = weight.n // 2 if epilogue == _lib.EPI_SILU_MUL else weight.n
-    lead = x.shape[:-1]
-    if out is None:
-        out = torch.empty((*lead, n_out), device=x.device, dtype=torch.bfloat16)
-    if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous bfloat16 [..., {n_out}] tensor")
-    res_ptr, ldr = None, 0
+    if out is not None:
+        _check_out(out, m, n_out, torch.bfloat16)
+    r2 = None
     if residual is not None:
-        _require_device(residual, "residual")
         r2, rm, ldr = _rows(residual, weight.n, "residual")
         if rm != m:
             raise ValueError(f"residual has {rm} rows, x has {m}")
-        res_ptr = r2.data_ptr()
+    _require_device(x, "x")
+    _require_device(weight.data, "weight")
+    if out is None:
+        out = torch.empty((*x.shape[:-1], n_out), device=x.device, dtype=torch.bfloat16)
+    _require_device(out, "out")
+    res_ptr, ldr = (None, 0) if r2 is None else (r2.data_ptr(), ldr)
+    if r2 is not None:
+        _require_device(r2, "residual")
     if isinstance(workspace, str):
         if workspace != "auto":
             raise ValueError(f"workspace must be 'auto', None or a tensor, not {workspace!r}")
@@ -123,28 +159,29 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weigh
     if not isinstance(weight, PackedWeight):
         raise ValueError("weight must be a PackedWeight (pack it with leanstack_amd.layout / leanserve)")
     lib = _lib.load()
-    _require_device(x, "x")
-    _require_device(weight.data, "weight")
-    _require_device(norm_weight, "norm_weight")
     x2, m, ldx = _rows(x, weight.k, "x")
     nw = norm_weight.reshape(-1)
     if nw.dtype != torch.bfloat16 or nw.numel() != weight.k:
         raise ValueError(f"norm_weight must be a bfloat16 [{weight.k}] tensor, got {nw.dtype} {tuple(norm_weight.shape)}")
-    if nw.stride(0) != 1 or nw.data_ptr() % 16:
-        nw = nw.contiguous() if nw.stride(0) != 1 else nw.clone()
     n_out = weight.n // 2 if epilogue == _lib.EPI_SILU_MUL else weight.n
-    lead = x.shape[:-1]
-    if out is None:
-        out = torch.empty((*lead, n_out), device=x.device, dtype=torch.bfloat16)
-    if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous bfloat16 [..., {n_out}] tensor")
-    res_ptr, ldr = None, 0
+    if out is not None:
+        _check_out(out, m, n_out, torch.bfloat16)
+    r2 = None
     if residual is not None:
-        _require_device(residual, "residual")
         r2, rm, ldr = _rows(residual, weight.n, "residual")
         if rm != m:
             raise ValueError(f"residual has {rm} rows, x has {m}")
-        res_ptr = r2.data_ptr()
+    _require_device(x, "x")
+    _require_device(weight.data, "weight")
+    _require_device(norm_weight, "norm_weight")
+    if nw.stride(0) != 1 or nw.data_ptr() % 16:
+        nw = nw.contiguous() if nw.stride(0) != 1 else nw.clone()
+    if out is None:
+        out = torch.empty((*x.shape[:-1], n_out), device=x.device, dtype=torch.bfloat16)
+    _require_device(out, "out")
+    res_ptr, ldr = (None, 0) if r2 is None else (r2.data_ptr(), ldr)
+    if r2 is not None:
+        _require_device(r2, "residual")
     status = lib.lsk_rmsnorm_linear_bf16(
         weight.data.data_ptr(), weight.layout, weight.n, weight.k,
         x2.data_ptr(), m, ldx,
@@ -156,25 +193,19 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weigh
     return out
 
 
-_attention_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_attention_workspaces: dict[int, torch.Tensor] = {}
 
 
 def attention_workspace(device: torch.device, n_q: int, n_kv: int, head_dim: int,
                         max_seq_len: int) -> torch.Tensor:
-    """The decode attention workspace for the current stream of `device`
-    (zero-filled once, left zero-filled by every call), large enough for
-    this geometry.  One per (device, stream): calls sharing one must be
-    stream-ordered."""
+    """The decode attention workspace of `device` (zero-filled once, left
+    zero-filled by every call), large enough for this geometry.  Calls
+    sharing it must be stream-ordered."""
     nbytes = _lib.load().lsk_attention_workspace_bytes(n_q, n_kv, head_dim, max_seq_len)
     if nbytes == 0:
         raise ValueError(f"no attention workspace for n_q={n_q}, n_kv={n_kv}, head_dim={head_dim}, "
                          f"max_seq_len={max_seq_len}")
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle() or 0)
-    ws = _attention_workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
-        _attention_workspaces[key] = ws
-    return ws
+    return _device_workspace(_attention_workspaces, device, nbytes, "attention")
 
 
 def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, eps: float,
@@ -265,22 +296,29 @@ def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: i
     if not isinstance(weight, PackedWeight) or weight.layout != _lib.LAYOUT_MFMA16X32:
         raise ValueError("lm_head weight must be a PackedWeight in the mfma16x32 layout")
     lib = _lib.load()
-    _require_device(hidden, "hidden")
     h2, m, ldx = _rows(hidden, weight.k, "hidden")
     v = weight.n
+    if out is not None and (out.dtype != torch.long or out.numel() < m or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous int64 tensor of at least {m} values "
+                         f"(got {out.dtype} {tuple(out.shape)})")
+    if logits_out is not None:
+        if logits_out.dtype != torch.float32 or logits_out.numel() != m * v or not logits_out.is_contiguous():
+            raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{v}")
+    if norm_weight is not None and (norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != weight.k):
+        raise ValueError(f"norm_weight must be a bfloat16 tensor of {weight.k} values")
+    _require_device(hidden, "hidden")
+    _require_device(weight.data, "weight")
     if workspace is None or workspace.m < m or workspace.v != v or workspace.k != weight.k:
         workspace = LmHeadWorkspace(m, v, weight.k, hidden.device)
     if out is None:
         out = torch.empty((m,), device=hidden.device, dtype=torch.long)
+    _require_device(out, "out")
     logits_ptr = None
     if logits_out is not None:
-        if logits_out.dtype != torch.float32 or logits_out.numel() != m * v or not logits_out.is_contiguous():
-            raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{v}")
+        _require_device(logits_out, "logits_out")
         logits_ptr = logits_out.data_ptr()
     if norm_weight is not None:
         _require_device(norm_weight, "norm_weight")
-        if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != weight.k:
-            raise ValueError(f"norm_weight must be a bfloat16 tensor of {weight.k} values")
         nw = norm_weight.reshape(-1).contiguous()
         status = lib.lsk_rmsnorm_lm_head_argmax_bf16(
             weight.data.data_ptr(), weight.layout, v, weight.k, h2.data_ptr(), m, ldx, nw.data_ptr(), float(eps),

@@ -1,139 +1,125 @@
-"""Static KV cache with the reference's interface (src/leanstack/runtime/kv_cache.py:8-35, :207-330).
+"""KV cache of the decode path, held in one region of the resident arena.
 
-`StaticKVBlockManager` keeps key and value tensors of shape
-[num_layers, batch_size, num_key_value_heads, max_seq_len, head_dim] and one
-sequence length per layer, as the reference's static manager does.  They may
-be views of the resident arena's `kv_cache` entry ([L, 2, B, n_kv, S, d]),
-so the cache lives in the same allocation as the weights.  The decode
-attention kernel (kernels.decode_attention) writes a token's k and v itself;
-`advance` then moves the layer's cursor, as `append` does after its copy.
+Storage is a single bf16 tensor ``[num_layers, 2, n_kv, capacity, head_dim]``
+-- for each layer its key block, then its value block -- normally the
+arena's ``kv_cache`` entry, so the cache lives in the same allocation as the
+weights.  Each block is a contiguous ``[n_kv, capacity, head_dim]`` tensor,
+the form the decode attention kernel addresses: the kernel writes a token's
+key and value row itself and the cache only moves the layer's cursor.
+
+The decode dispatch reads three things from a cache (the static-cache
+interface of the reference runtime, src/leanstack/runtime/kv_cache.py:207-266):
+``layer_seq_lens[layer]``, ``layer_tensors(layer)`` and ``advance(layer, n)``.
+Rows produced by the torch glue (prefill and verify blocks) enter through
+``write_rows``; a speculative verify that rejects drafted tokens rolls the
+cursors back with ``mark`` / ``rewind``
+(experiments/models/qwen_explicit_runtime_loop.py:822-847).  Batch 1 only:
+the decode kernels serve one sequence.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
-
 import torch
 
 
-@dataclass(frozen=True)
-class KVPageLayout:
-    """Geometry of the cache (src/leanstack/runtime/kv_cache.py:8-35)."""
+class ArenaKVCache:
+    """Per-layer key/value blocks over one storage tensor, with a row cursor per layer.
 
-    num_layers: int
-    num_key_value_heads: int
-    head_dim: int
-    page_size: int
-    max_seq_len: int
-    batch_size: int
-    dtype: torch.dtype
-    device: torch.device
+    storage: None to allocate zero-filled blocks on `device`, or an existing
+    ``[L, 2, n_kv, capacity, d]`` tensor (a ``[L, 2, 1, n_kv, capacity, d]``
+    arena entry with its batch axis of 1 is accepted too) that the cache
+    then works in place."""
 
-    def __post_init__(self) -> None:
-        if self.page_size <= 0:
-            raise ValueError("page_size must be positive")
-        if self.max_seq_len <= 0:
-            raise ValueError("max_seq_len must be positive")
-        if self.batch_size <= 0:
-            raise ValueError("batch_size must be positive")
+    def __init__(self, num_layers: int, num_key_value_heads: int, head_dim: int, capacity: int, *,
+                 storage: torch.Tensor | None = None, device: torch.device | str = "cpu",
+                 dtype: torch.dtype = torch.bfloat16) -> None:
+        dims = (num_layers, num_key_value_heads, head_dim, capacity)
+        if min(dims) < 1:
+            raise ValueError(f"cache dimensions must all be >= 1 (layers, kv heads, head_dim, capacity) = {dims}")
+        shape = (num_layers, 2, num_key_value_heads, capacity, head_dim)
+        if storage is None:
+            storage = torch.zeros(shape, device=device, dtype=dtype)
+        else:
+            if storage.dim() == 6 and storage.shape[2] == 1:
+                storage = storage[:, :, 0]
+            if tuple(storage.shape) != shape or not storage.is_contiguous():
+                raise ValueError(f"cache storage must be a contiguous {list(shape)} tensor "
+                                 f"(layers, key|value, kv heads, rows, head_dim); got {list(storage.shape)}")
+        self.storage = storage
+        self.capacity = capacity
+        self.layer_seq_lens = [0] * num_layers
+
+    @classmethod
+    def from_arena(cls, arena, num_key_value_heads: int, head_dim: int) -> "ArenaKVCache":
+        """The cache over a resident arena's `kv_cache` entry."""
+        region = arena.view("kv_cache")
+        if region.dim() != 6 or region.shape[2] != 1:
+            raise ValueError(f"the arena's kv_cache entry {list(region.shape)} is not a batch-1 cache")
+        return cls(region.shape[0], num_key_value_heads, head_dim, region.shape[4], storage=region)
+
+    # -- what the decode dispatch reads --------------------------------------
+
+    def layer_tensors(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The layer's whole key and value blocks, [n_kv, capacity, d] each."""
+        return self.storage[layer, 0], self.storage[layer, 1]
+
+    def advance(self, layer: int, rows: int) -> None:
+        """Count `rows` rows written after the layer's cursor (by the decode
+        attention kernel or write_rows)."""
+        new = self.layer_seq_lens[layer] + rows
+        if rows < 0 or new > self.capacity:
+            raise ValueError(f"layer {layer}: cursor {self.layer_seq_lens[layer]} + {rows} rows does not fit "
+                             f"the {self.capacity}-row cache")
+        self.layer_seq_lens[layer] = new
+
+    # -- the torch glue's side -----------------------------------------------
 
     @property
-    def num_pages(self) -> int:
-        return (self.max_seq_len + self.page_size - 1) // self.page_size
+    def key_cache(self) -> torch.Tensor:
+        """All key blocks with a batch axis of 1, [L, 1, n_kv, capacity, d]."""
+        return self.storage[:, 0].unsqueeze(1)
 
-    def pages_for_tokens(self, token_count: int) -> int:
-        if token_count <= 0:
-            return 0
-        return (token_count + self.page_size - 1) // self.page_size
+    @property
+    def value_cache(self) -> torch.Tensor:
+        return self.storage[:, 1].unsqueeze(1)
 
+    @property
+    def max_layer_seq_len(self) -> int:
+        return max(self.layer_seq_lens)
 
-@dataclass(frozen=True)
-class StaticKVCursorSnapshot:
-    layer_seq_lens: tuple[int, ...]
-    max_layer_seq_len: int
+    def rows(self, layer: int) -> int:
+        return self.layer_seq_lens[layer]
 
+    def write_rows(self, layer: int, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Copy key / value rows ([n_kv, T, d], or [1, n_kv, T, d]) to the
+        layer's cursor and move it past them.  Nothing moves if they do not
+        fit."""
+        k_block, v_block = self.layer_tensors(layer)
+        keys = keys[0] if keys.dim() == 4 and keys.shape[0] == 1 else keys
+        values = values[0] if values.dim() == 4 and values.shape[0] == 1 else values
+        if keys.shape != values.shape or keys.dim() != 3 or keys.shape[0] != k_block.shape[0] \
+                or keys.shape[2] != k_block.shape[2]:
+            raise ValueError(f"keys {list(keys.shape)} and values {list(values.shape)} must both be "
+                             f"[{k_block.shape[0]}, rows, {k_block.shape[2]}]")
+        start = self.layer_seq_lens[layer]
+        self.advance(layer, keys.shape[1])
+        k_block[:, start : start + keys.shape[1]].copy_(keys)
+        v_block[:, start : start + keys.shape[1]].copy_(values)
 
-class StaticKVBlockManager:
-    """Static KV cache (src/leanstack/runtime/kv_cache.py:207-330).
+    def attended(self, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The layer's written rows as [1, n_kv, rows, d] views (what the
+        torch glue attends over)."""
+        k_block, v_block = self.layer_tensors(layer)
+        n = self.layer_seq_lens[layer]
+        return k_block[None, :, :n], v_block[None, :, :n]
 
-    storage: None (zero-filled tensors of the layout's shape are allocated),
-    or a [num_layers, 2, batch_size, n_kv, max_seq_len, head_dim] tensor whose
-    [:, 0] / [:, 1] halves become the key / value caches (the arena's
-    `kv_cache` entry)."""
+    def mark(self) -> tuple[int, ...]:
+        """The cursors now, for rewind()."""
+        return tuple(self.layer_seq_lens)
 
-    def __init__(self, layout: KVPageLayout, storage: torch.Tensor | None = None):
-        self.layout = layout
-        shape = (layout.num_layers, layout.batch_size, layout.num_key_value_heads, layout.max_seq_len,
-                 layout.head_dim)
-        if storage is None:
-            self.key_cache = torch.zeros(shape, device=layout.device, dtype=layout.dtype)
-            self.value_cache = torch.zeros(shape, device=layout.device, dtype=layout.dtype)
-        else:
-            expect = (layout.num_layers, 2) + shape[1:]
-            if tuple(storage.shape) != expect or storage.dtype != layout.dtype:
-                raise ValueError(f"storage must be {layout.dtype} {expect}, got {storage.dtype} {tuple(storage.shape)}")
-            self.key_cache = storage[:, 0]
-            self.value_cache = storage[:, 1]
-        self.layer_seq_lens = [0 for _ in range(layout.num_layers)]
-        self.max_layer_seq_len = 0
-
-    def append(self, layer_idx: int, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        """Copy [B, n_kv, T, d] key / value states after the layer's cached rows."""
-        if key_states.shape != value_states.shape:
-            raise ValueError("key/value states must have the same shape")
-        batch_size, num_heads, token_count, head_dim = key_states.shape
-        if batch_size != self.layout.batch_size:
-            raise ValueError(f"expected batch_size={self.layout.batch_size}, got {batch_size}")
-        if num_heads != self.layout.num_key_value_heads:
-            raise ValueError(f"expected num_key_value_heads={self.layout.num_key_value_heads}, got {num_heads}")
-        if head_dim != self.layout.head_dim:
-            raise ValueError(f"expected head_dim={self.layout.head_dim}, got {head_dim}")
-        start = self.layer_seq_lens[layer_idx]
-        end = start + token_count
-        if end > self.layout.max_seq_len:
-            raise ValueError(
-                f"cache overflow for layer {layer_idx}: requested {end} tokens with max_seq_len={self.layout.max_seq_len}"
-            )
-        self.key_cache[layer_idx, :, :, start:end, :].copy_(key_states)
-        self.value_cache[layer_idx, :, :, start:end, :].copy_(value_states)
-        self.advance(layer_idx, token_count)
-
-    def advance(self, layer_idx: int, token_count: int) -> None:
-        """Count `token_count` rows written after the layer's cached ones."""
-        end = self.layer_seq_lens[layer_idx] + token_count
-        if end > self.layout.max_seq_len:
-            raise ValueError(f"cache overflow for layer {layer_idx}: {end} > max_seq_len={self.layout.max_seq_len}")
-        self.layer_seq_lens[layer_idx] = end
-        self.max_layer_seq_len = max(self.max_layer_seq_len, end)
-
-    def append_and_get(self, layer_idx: int, key_states: torch.Tensor,
-                       value_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        self.append(layer_idx, key_states, value_states)
-        return self.get(layer_idx)
-
-    def get(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
-        seq_len = self.layer_seq_lens[layer_idx]
-        return self.key_cache[layer_idx, :, :, :seq_len, :], self.value_cache[layer_idx, :, :, :seq_len, :]
-
-    def layer_tensors(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """The layer's whole [n_kv, max_seq_len, head_dim] key / value caches
-        (batch 1), as the decode attention kernel addresses them."""
-        if self.layout.batch_size != 1:
-            raise ValueError("the decode attention kernel serves batch 1")
-        return self.key_cache[layer_idx, 0], self.value_cache[layer_idx, 0]
-
-    def get_layer_seq_length(self, layer_idx: int) -> int:
-        return self.layer_seq_lens[layer_idx]
-
-    def get_seq_length(self) -> int:
-        return self.max_layer_seq_len
-
-    def page_table(self, layer_idx: int) -> tuple[int, ...]:
-        return tuple(range(self.layout.pages_for_tokens(self.get_layer_seq_length(layer_idx))))
-
-    def snapshot_cursor(self) -> StaticKVCursorSnapshot:
-        return StaticKVCursorSnapshot(tuple(int(n) for n in self.layer_seq_lens), int(self.max_layer_seq_len))
-
-    def restore_cursor(self, snapshot: StaticKVCursorSnapshot) -> None:
-        self.layer_seq_lens = list(snapshot.layer_seq_lens)
-        self.max_layer_seq_len = int(snapshot.max_layer_seq_len)
+    def rewind(self, mark: tuple[int, ...]) -> None:
+        """Move the cursors back to `mark`: rows written since are dropped
+        (and overwritten by the next writes)."""
+        if len(mark) != len(self.layer_seq_lens) or any(m > n or m < 0 for m, n in zip(mark, self.layer_seq_lens)):
+            raise ValueError(f"mark {mark} is not an earlier state of the cursors {tuple(self.layer_seq_lens)}")
+        self.layer_seq_lens = list(mark)

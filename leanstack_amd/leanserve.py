@@ -250,6 +250,10 @@ class ResidentArena:
         self.buffer = raw[skew : skew + plan.arena_bytes]
         self._index = {e.name: e for e in plan.entries}
 
+    def weight_names(self) -> set[str]:
+        """Entries a pack must fill: everything but scratch and the KV cache."""
+        return {e.name for e in self.plan.entries if e.role not in ("scratch", "kv_cache")}
+
     def view(self, name: str) -> torch.Tensor:
         e = self._index[name]
         raw = self.buffer[e.offset : e.end]
@@ -276,12 +280,25 @@ class ResidentArena:
 
     def store_packed(self, name: str, packed: torch.Tensor) -> None:
         e = self._index[name]
-        if e.layout is None or packed.numel() * 2 != e.nbytes:
-            raise ValueError(f"{name}: not a packed entry of {e.nbytes} bytes")
+        if e.layout is None or packed.dtype != torch.bfloat16 or packed.numel() * 2 != e.nbytes:
+            raise ValueError(f"{name}: not a bfloat16 packed entry of {e.nbytes} bytes")
         self.buffer[e.offset : e.end].view(torch.bfloat16).copy_(packed.reshape(-1))
 
 
 # ----------------------------------------------------------------- loading
+
+
+def _check_entry_layout(entry: ArenaEntry, layout_name: str, logical_shape) -> None:
+    """A pack tensor may fill a planned entry only in the entry's own layout
+    and logical shape (a gate_up stored as plain mfma16x32, or a row-major
+    tensor where a packed one is planned, is refused)."""
+    from .layout import LAYOUT_IDS
+
+    expect = "rowmajor" if entry.layout is None else next(n for n, i in LAYOUT_IDS.items() if i == entry.layout)
+    if layout_name != expect:
+        raise ValueError(f"{entry.name}: the pack stores layout {layout_name!r}, the plan needs {expect!r}")
+    if tuple(logical_shape) != tuple(entry.shape):
+        raise ValueError(f"{entry.name}: the pack's shape {list(logical_shape)} != planned {list(entry.shape)}")
 
 
 def materialize_qwen_semantic_stack_from_leanpack(
@@ -312,11 +329,14 @@ def materialize_qwen_semantic_stack_from_leanpack(
     g = geometry_from_manifest(manifest)
     plan = build_resident_buffer_plan(g, buckets=buckets, max_rows=max_rows, include_lm_head=include_output_head)
     arena = ResidentArena(plan, device)
-    planned = {e.name for e in plan.entries}
     by_file: dict[str, list] = {}
     for t in manifest.tensors:
-        if t.name in planned:
+        if t.name in arena.weight_names():
+            _check_entry_layout(plan.entry(t.name), t.layout, t.logical_shape)
             by_file.setdefault(t.file, []).append(t)
+    missing = sorted(arena.weight_names() - {t.name for ts in by_file.values() for t in ts})
+    if missing:
+        raise ValueError(f"{root}: the pack has no tensor for {len(missing)} planned weights, e.g. {missing[:3]}")
     for file_name, entries in by_file.items():
         with safe_open(str(root / file_name), framework="pt", device="cpu") as handle:
             for t in entries:

@@ -142,7 +142,7 @@ class DecodeLinearStack:
 class DecodeStep:
     """One whole decode token (M = 1) over every layer, in the reference's
     order (semantic_qwen_decode_layer_forward, qwen_explicit.py:1247-1272,
-    then the greedy head :952-960): per layer input_layernorm + QKV, the
+    then the greedy head, :1798-1832): per layer input_layernorm + QKV, the
     attention kernel (q/k norms, RoPE, cache append, GQA attention), o_proj
     + residual, post_attention_layernorm + gate_up + SiLU*up, down +
     residual; then the final RMSNorm and the lm_head argmax.  All buffers are
@@ -156,8 +156,13 @@ class DecodeStep:
 
     def __init__(self, layers: list[LayerProjections], norms: torch.Tensor, qk_norms: torch.Tensor,
                  final_norm: torch.Tensor, lm_head: PackedWeight, geometry: QwenGeometry, k_cache: torch.Tensor,
-                 v_cache: torch.Tensor, device: torch.device) -> None:
+                 v_cache: torch.Tensor, device: torch.device, logits_mode: int = _lib.LOGITS_FP32) -> None:
         g = geometry
+        # The head compares fp32 scores by default, as the reference's decode
+        # loop does with its default "auto" backend (select_semantic_greedy_token
+        # -> the cuTile head, qwen_explicit.py:1798-1832); LOGITS_BF16 is the
+        # torch.mv head of _semantic_greedy_head_vector (:952-960).
+        self.logits_mode = logits_mode
         self.layers, self.norms, self.qk_norms, self.final_norm, self.lm_head = layers, norms, qk_norms, final_norm, \
             lm_head
         self.g, self.k_cache, self.v_cache, self.device = g, k_cache, v_cache, device
@@ -178,8 +183,11 @@ class DecodeStep:
         ws_bytes = _lib.load().lsk_attention_workspace_bytes(g.num_attention_heads, g.num_key_value_heads,
                                                                g.head_dim, max_seq)
         self.attn_ws = torch.zeros(ws_bytes, device=device, dtype=torch.uint8)  # left zeroed by every launch
-        self.token = torch.empty((1,), device=device, dtype=torch.long)
+        self.token = torch.zeros((1,), device=device, dtype=torch.long)
         self.pos_dev = torch.zeros((1,), device=device, dtype=torch.int32)
+        # device-side indices of launch_next, clamped into their tables
+        self._row = torch.zeros((1,), device=device, dtype=torch.long)
+        self._slot = torch.zeros((1,), device=device, dtype=torch.long)
 
     def set_position(self, pos: int) -> None:
         """Write the position launch() reads, ordered on the current stream
@@ -195,13 +203,26 @@ class DecodeStep:
         self.token becomes the input, the token at position self.pos_dev is
         computed (tokens_out[pos] = the new token, when given), and the
         position advances by one.  embedding: [V, H] bf16 (the tied lm_head's
-        row-major copy serves)."""
+        row-major copy serves).
+
+        Replay bound: a sequence has max_seq_len positions.  Replays past the
+        last one leave every cache untouched (the attention kernel ignores a
+        position outside the cache) and write their token to the last slot of
+        tokens_out; the device indices are clamped, so no replay reads or
+        writes outside the embedding table or tokens_out.  The argmax kernels
+        always return a valid vocab row (NaN and -inf scores included)."""
         if embedding.dim() != 2 or embedding.shape[1] != self.g.hidden_size or embedding.dtype != torch.bfloat16:
             raise ValueError(f"embedding must be a bfloat16 [V, {self.g.hidden_size}] tensor")
-        torch.index_select(embedding, 0, self.token, out=self.hidden[0])
+        if tokens_out is not None and (tokens_out.dtype != torch.long or tokens_out.dim() != 1
+                                       or tokens_out.numel() < 1 or tokens_out.device != self.pos_dev.device):
+            raise ValueError("tokens_out must be a 1-D int64 tensor on the step's device")
+        torch.clamp(self.token, 0, embedding.shape[0] - 1, out=self._row)
+        torch.index_select(embedding, 0, self._row, out=self.hidden[0])
         self.launch()
         if tokens_out is not None:
-            tokens_out.index_copy_(0, self.pos_dev.long(), self.token)
+            self._slot.copy_(self.pos_dev)
+            self._slot.clamp_(0, tokens_out.numel() - 1)
+            tokens_out.index_copy_(0, self._slot, self.token)
         self.pos_dev.add_(1)
 
     def launch(self, pos: int | None = None) -> None:
@@ -227,6 +248,6 @@ class DecodeStep:
                                    out=self.act)
             kernels.linear(self.act, p.down, epilogue=_lib.EPI_RESIDUAL_ADD, residual=self.mid, out=y)
         last = self.hidden[len(self.layers) % 2]
-        # final RMSNorm + bf16 logits + argmax (qwen_explicit.py:952-960) in the lm_head kernel
-        kernels.lm_head_argmax(last, self.lm_head, logits_mode=_lib.LOGITS_BF16, workspace=self.head_ws,
+        # final RMSNorm + scores + argmax (qwen_explicit.py:1798-1832 / :952-960) in the lm_head kernel
+        kernels.lm_head_argmax(last, self.lm_head, logits_mode=self.logits_mode, workspace=self.head_ws,
                                out=self.token, norm_weight=self.final_norm, eps=self.eps)

@@ -47,3 +47,29 @@ def bits(t: torch.Tensor) -> np.ndarray:
 
 def from_bits(b: np.ndarray) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16)
+
+
+def assert_greedy_rows(idx: torch.Tensor, ref_scores: torch.Tensor, got_scores: torch.Tensor, what: str = "") -> None:
+    """Greedy tokens against the oracle's scores, unconditionally.
+
+    delta = the largest |kernel score - oracle score| over the vocab (the
+    kernel's own scores, read back).  Where the oracle's top-1 margin exceeds
+    2*delta no score perturbation of that size can change the argmax, so the
+    token must equal the oracle's; otherwise it must be one of the oracle's
+    near-maximal tokens (within 2*delta of the top score), of which the
+    oracle's top-2 are the usual pair."""
+    ref_scores = ref_scores.float().reshape(-1, ref_scores.shape[-1])
+    got_scores = got_scores.float().reshape(ref_scores.shape)
+    idx = idx.reshape(-1)
+    for row in range(ref_scores.shape[0]):
+        s = ref_scores[row]
+        delta = float((got_scores[row] - s).abs().max())
+        top = torch.topk(s, 2)
+        margin = float(top.values[0] - top.values[1])
+        token = int(idx[row])
+        print(f"{what} row {row}: token {token}, oracle {int(top.indices[0])}, margin {margin:.4g}, delta {delta:.3g}")
+        if margin > 2 * delta:
+            assert token == int(top.indices[0]), f"{what} row {row}: {token} != {int(top.indices[0])}"
+        else:
+            near = torch.nonzero(s >= top.values[0] - 2 * delta).view(-1).tolist()
+            assert token in near, f"{what} row {row}: {token} not among the near-maximal {near[:8]}"

@@ -220,3 +220,46 @@ def test_product_package_does_not_import_the_oracle():
     for path in (REPO / "leanstack_amd").rglob("*.py"):
         text = path.read_text(encoding="utf-8")
         assert "import oracle" not in text and "from oracle" not in text, path
+
+
+def test_wrappers_refuse_outputs_of_the_wrong_size():
+    """A caller's `out` must hold exactly what the kernel writes: the C layer
+    sees only a pointer, so x[5, K] with out[1, N] would write 4 rows past the
+    allocation.  The wrappers check sizes before anything reaches the device
+    (CPU tensors here: the size check comes first)."""
+    from leanstack_amd import kernels
+    from leanstack_amd.layout import PackedWeight
+
+    w = PackedWeight(torch.zeros(64 * 64, dtype=torch.bfloat16), 64, 64, _lib.LAYOUT_MFMA16X32)
+    x = torch.zeros((5, 64), dtype=torch.bfloat16)
+    for bad in (torch.empty((1, 64), dtype=torch.bfloat16), torch.empty((5, 64), dtype=torch.float32),
+                torch.empty((5, 128), dtype=torch.bfloat16)[:, :64], torch.empty((6, 64), dtype=torch.bfloat16)):
+        with pytest.raises(ValueError, match="out must be"):
+            kernels.linear(x, w, out=bad)
+        with pytest.raises(ValueError, match="out must be"):
+            kernels.rmsnorm_linear(x, torch.ones(64, dtype=torch.bfloat16), 1e-6, w, out=bad)
+    for bad in (torch.empty(4, dtype=torch.long), torch.empty(5, dtype=torch.int32),
+                torch.empty((5, 2), dtype=torch.long)[:, 0]):
+        with pytest.raises(ValueError, match="out must be"):
+            kernels.lm_head_argmax(x, w, out=bad)
+    with pytest.raises(ValueError, match="residual has"):
+        kernels.linear(x, w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=torch.zeros((4, 64), dtype=torch.bfloat16))
+    # right sizes pass the size checks and stop at the device check
+    with pytest.raises(ValueError, match="GPU tensor"):
+        kernels.linear(x, w, out=torch.empty((5, 64), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU tensor"):
+        kernels.lm_head_argmax(x, w, out=torch.empty(8, dtype=torch.long))
+
+
+def test_launch_next_refuses_a_bad_token_buffer():
+    """DecodeStep.launch_next's token buffer: 1-D int64 on the step's device."""
+    from leanstack_amd.stack import DecodeStep
+
+    step = DecodeStep.__new__(DecodeStep)
+    step.g = type("G", (), {"hidden_size": 64})()
+    step.pos_dev = torch.zeros(1, dtype=torch.int32)
+    emb = torch.zeros((16, 64), dtype=torch.bfloat16)
+    for bad in (torch.zeros(4, dtype=torch.int32), torch.zeros((2, 2), dtype=torch.long),
+                torch.zeros(0, dtype=torch.long)):
+        with pytest.raises(ValueError, match="tokens_out"):
+            step.launch_next(emb, bad)

@@ -16,7 +16,7 @@ from leanstack_amd.geometry import QWEN3_4B as G
 from leanstack_amd.layout import PackedWeight
 from oracle import brute
 from oracle import projections as ref
-from tests.helpers import activations, assert_parity, bits, weight
+from tests.helpers import activations, assert_greedy_rows, assert_parity, bits, weight
 
 pytestmark = pytest.mark.gpu
 
@@ -64,8 +64,10 @@ def test_decode_projection(gpu, name, m):
     assert_parity(y, expect, f"{name} M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 16])
 def test_decode_gate_up_silu(gpu, m):
+    """Every M of the gate_up decode forms (4 waves x 10 pairs up to M = 2,
+    then 8 x 5 with 1..5 staged chunks per lane, and the 16-row kernel)."""
     n, k = 2 * G.intermediate_size, G.hidden_size
     w = weight(n, k, seed=20 + m)
     x = activations(m, k, seed=200 + m)
@@ -134,15 +136,7 @@ def test_lm_head_argmax_fp32(gpu, m):
     logits = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
     idx = kernels.lm_head_argmax(h.to(dev), pw, logits_out=logits).cpu()
     scores = ref.logits_scores_fp32(h, e)
-    expect = scores.argmax(dim=-1)
-    margin = ref.top2_margin(scores)
-    print(f"M={m} idx={idx.tolist()} margin={margin.tolist()}")
-    top2 = scores.topk(2, dim=-1).indices
-    for row in range(m):
-        if margin[row] > 1e-3:  # a clear winner: the same index
-            assert idx[row] == expect[row], f"row {row}"
-        else:  # a near tie (fp32 summation order decides): one of the two
-            assert idx[row] in top2[row].tolist(), f"row {row}"
+    assert_greedy_rows(idx, scores, logits.cpu(), f"lm_head fp32 M={m}")
     assert_parity(logits.cpu(), scores, "lm_head fp32 logits")
 
 
@@ -160,13 +154,7 @@ def test_rmsnorm_lm_head_argmax(gpu, m):
     logits = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
     idx = kernels.lm_head_argmax(h.to(dev), pw, logits_out=logits, norm_weight=nw.to(dev), eps=1e-6).cpu()
     scores = ref.logits_scores_fp32(ref.rmsnorm(h, nw, 1e-6), e)
-    margin = ref.top2_margin(scores)
-    top2 = scores.topk(2, dim=-1).indices
-    for row in range(m):
-        if margin[row] > 1e-2:
-            assert idx[row] == scores[row].argmax(), f"row {row}"
-        else:
-            assert idx[row] in top2[row].tolist(), f"row {row}"
+    assert_greedy_rows(idx, scores, logits.cpu(), f"rmsnorm lm_head M={m}")
     assert_parity(logits.cpu(), scores, f"rmsnorm lm_head M={m} logits")
 
 
@@ -331,3 +319,64 @@ def test_prefill_m8192_sampled_rows(gpu, name):
     rows = torch.cat([torch.tensor([0, 1, 255, 256, 4095, 4096, 8190, 8191]),
                       torch.randint(0, m, (56,), generator=gen)]).unique()
     assert_parity(y[rows], _oracle(x[rows], w, epi), f"{name} prefill M=8192 (rows sampled)")
+
+
+def test_lm_head_argmax_follows_torch_on_nan_and_inf(gpu):
+    """Scores that are NaN, +inf or all -inf: the kernel's token is what
+    torch.argmax returns on the same scores (the first NaN wins, +inf beats
+    any finite score, an all -inf row gives index 0), in both logit modes --
+    never an index outside the vocab."""
+    v, k = 4096, 256
+    dev = torch.device("cuda:0")
+    h = activations(1, k, seed=730).abs() + 0.5  # positive, so a row's sign fixes its score's sign
+    cases = {}
+    e = weight(v, k, seed=731)
+    e[3000] = float("nan")
+    e[1500] = float("nan")
+    e[200] = float("inf")
+    cases["nan rows"] = e
+    e = weight(v, k, seed=732)
+    e[2222] = float("inf")
+    e[3333] = float("inf")
+    cases["inf rows"] = e
+    cases["all -inf"] = torch.full((v, k), float("-inf"), dtype=torch.bfloat16)
+    for what, e in cases.items():
+        expect = int(ref.logits_scores_fp32(h, e).argmax(dim=-1))
+        pw = PackedWeight.from_rowmajor(e.to(dev))
+        for mode in (_lib.LOGITS_FP32, _lib.LOGITS_BF16):
+            idx = kernels.lm_head_argmax(h.to(dev), pw, logits_mode=mode).cpu()
+            assert idx.tolist() == [expect], (what, mode, idx.tolist(), expect)
+    assert [int(ref.logits_scores_fp32(h, e).argmax(dim=-1)) for e in cases.values()] == [1500, 2222, 0]
+
+
+def test_split_k_lost_wait_is_reported_and_poisons(gpu):
+    """A split-K workgroup whose bounded wait gives up (forced from the host
+    with a wait limit of 0 polls: every chunk that is not the last to arrive
+    stops waiting at once) sets the workspace's error word and writes NaN to
+    its share of the block instead of a partial sum; tiles of chunks that did
+    complete match the oracle, and the flags are left clear.  With the limit
+    restored the next call is whole again."""
+    dev = torch.device("cuda:0")
+    m, n, k = 2048, G.hidden_size, G.intermediate_size  # 80 blocks, each split in 3 K chunks
+    w = weight(n, k, seed=86)
+    x = activations(m, k, seed=860)
+    pw = PackedWeight.from_rowmajor(w.to(dev))
+    ws = torch.zeros(_lib.load().lsk_workspace_bytes(_lib.OP_LINEAR, m, n, k), device=dev, dtype=torch.uint8)
+    expect = ref.linear(x, w)
+    try:
+        kernels.set_linear_wait_limit(0)
+        y = kernels.linear(x.to(dev), pw, workspace=ws)
+        torch.cuda.synchronize()
+    finally:
+        kernels.set_linear_wait_limit(kernels.LINEAR_WAIT_LIMIT_DEFAULT)
+    assert kernels.linear_error(ws) != 0
+    y = y.cpu()
+    bad = torch.isnan(y.float())
+    print(f"NaN outputs after forced give-ups: {int(bad.sum())} of {y.numel()}")
+    assert bad.any()
+    assert_parity(y[~bad], expect[~bad], "split-K tiles that completed")
+    assert int(ws[256:8192].view(torch.int32).abs().sum().item()) == 0
+    y2 = kernels.linear(x.to(dev), pw, workspace=ws)
+    torch.cuda.synchronize()
+    assert kernels.linear_error(ws) == 0
+    assert_parity(y2.cpu(), expect, "split-K after the limit is restored")

@@ -1,113 +1,120 @@
-"""The static KV cache manager on the CPU (leanstack_amd/kv_cache.py): the
-reference's StaticKVBlockManager contract (src/leanstack/runtime/kv_cache.py:
-207-330) and the two additions the decode attention kernel relies on
-(`layer_tensors`, `advance`)."""
+"""The arena KV cache on the CPU (leanstack_amd/kv_cache.py): what the decode
+dispatch reads from it (layer_seq_lens, layer_tensors, advance), the rows
+the torch glue writes, and the speculative rollback."""
 
 from __future__ import annotations
 
 import pytest
 import torch
 
-from leanstack_amd.kv_cache import KVPageLayout, StaticKVBlockManager
+from leanstack_amd import dispatch
+from leanstack_amd.kv_cache import ArenaKVCache
 
 
-def _layout(**over):
-    kw = dict(num_layers=3, num_key_value_heads=2, head_dim=8, page_size=4, max_seq_len=10, batch_size=1,
-              dtype=torch.bfloat16, device=torch.device("cpu"))
-    kw.update(over)
-    return KVPageLayout(**kw)
-
-
-def _states(t, seed, b=1, h=2, d=8):
+def _rows(t, seed, h=2, d=8):
     g = torch.Generator().manual_seed(seed)
-    return (torch.randn((b, h, t, d), generator=g).to(torch.bfloat16),
-            torch.randn((b, h, t, d), generator=g).to(torch.bfloat16))
+    return (torch.randn((h, t, d), generator=g).to(torch.bfloat16),
+            torch.randn((h, t, d), generator=g).to(torch.bfloat16))
 
 
-def test_layout_rejects_bad_geometry():
-    for over in (dict(page_size=0), dict(max_seq_len=0), dict(batch_size=0)):
+def _cache(**over):
+    kw = dict(num_layers=3, num_key_value_heads=2, head_dim=8, capacity=10)
+    kw.update(over)
+    return ArenaKVCache(**kw)
+
+
+def test_rejects_empty_dimensions():
+    for over in (dict(num_layers=0), dict(num_key_value_heads=0), dict(head_dim=0), dict(capacity=0)):
         with pytest.raises(ValueError):
-            _layout(**over)
+            _cache(**over)
 
 
-def test_append_get_and_lengths():
-    cache = StaticKVBlockManager(_layout())
-    k1, v1 = _states(3, 1)
-    k, v = cache.append_and_get(1, k1, v1)
-    assert torch.equal(k, k1) and torch.equal(v, v1)
-    k2, v2 = _states(2, 2)
-    cache.append(1, k2, v2)
-    k, v = cache.get(1)
-    assert torch.equal(k, torch.cat((k1, k2), dim=2)) and torch.equal(v, torch.cat((v1, v2), dim=2))
-    assert cache.get_layer_seq_length(1) == 5 and cache.get_layer_seq_length(0) == 0
-    assert cache.get_seq_length() == 5
-    assert cache.page_table(1) == (0, 1)  # 5 rows in pages of 4
-    assert cache.get(0)[0].shape == (1, 2, 0, 8)
+def test_write_rows_and_cursors():
+    cache = _cache()
+    k1, v1 = _rows(3, 1)
+    cache.write_rows(1, k1, v1)
+    k2, v2 = _rows(2, 2)
+    cache.write_rows(1, k2[None], v2[None])  # a batch axis of 1 is accepted
+    k, v = cache.attended(1)
+    assert k.shape == (1, 2, 5, 8)
+    assert torch.equal(k[0], torch.cat((k1, k2), dim=1)) and torch.equal(v[0], torch.cat((v1, v2), dim=1))
+    assert cache.rows(1) == 5 and cache.rows(0) == 0 and cache.max_layer_seq_len == 5
+    assert cache.attended(0)[0].shape == (1, 2, 0, 8)
 
 
-def test_append_rejects_mismatched_states_and_overflow():
-    cache = StaticKVBlockManager(_layout())
-    k, v = _states(3, 3)
+def test_refuses_rows_that_do_not_fit():
+    cache = _cache()
+    k, v = _rows(3, 3)
     with pytest.raises(ValueError):
-        cache.append(0, k, v[:, :, :2])
+        cache.write_rows(0, k, v[:, :2])
     with pytest.raises(ValueError):
-        cache.append(0, *_states(3, 4, h=3))
+        cache.write_rows(0, *_rows(3, 4, h=3))
     with pytest.raises(ValueError):
-        cache.append(0, *_states(3, 5, d=4))
-    with pytest.raises(ValueError):
-        cache.append(0, *_states(3, 6, b=2))
-    cache.append(0, *_states(9, 7))
-    with pytest.raises(ValueError, match="overflow"):
-        cache.append(0, *_states(2, 8))
-    assert cache.get_layer_seq_length(0) == 9  # a refused append moves nothing
-    with pytest.raises(ValueError, match="overflow"):
+        cache.write_rows(0, *_rows(3, 5, d=4))
+    cache.write_rows(0, *_rows(9, 7))
+    before = cache.storage.clone()
+    with pytest.raises(ValueError, match="does not fit"):
+        cache.write_rows(0, *_rows(2, 8))
+    assert cache.rows(0) == 9 and torch.equal(cache.storage, before)  # a refused write moves nothing
+    with pytest.raises(ValueError, match="does not fit"):
         cache.advance(0, 2)
+    with pytest.raises(ValueError):
+        cache.advance(0, -1)
     cache.advance(0, 1)
-    assert cache.get_layer_seq_length(0) == 10
+    assert cache.rows(0) == 10
 
 
-def test_snapshot_restore_rolls_back_the_cursor():
-    """The speculative verify rollback (qwen_explicit_runtime_loop.py:822-847):
-    rows written after the snapshot are forgotten, earlier ones kept."""
-    cache = StaticKVBlockManager(_layout())
-    k1, v1 = _states(2, 9)
+def test_mark_and_rewind():
+    """Rows written after a mark are dropped by rewind and overwritten by the
+    next write; earlier rows stay."""
+    cache = _cache()
+    k1, v1 = _rows(2, 9)
     for layer in range(3):
-        cache.append(layer, k1, v1)
-    snap = cache.snapshot_cursor()
+        cache.write_rows(layer, k1, v1)
+    mark = cache.mark()
     for layer in range(3):
-        cache.append(layer, *_states(4, 10 + layer))
-    assert cache.get_seq_length() == 6
-    cache.restore_cursor(snap)
-    assert [cache.get_layer_seq_length(i) for i in range(3)] == [2, 2, 2] and cache.get_seq_length() == 2
-    assert torch.equal(cache.get(2)[0], k1)
-    k3, v3 = _states(1, 20)
-    cache.append(2, k3, v3)  # overwrites row 2 of layer 2
-    assert torch.equal(cache.get(2)[1], torch.cat((v1, v3), dim=2))
+        cache.write_rows(layer, *_rows(4, 10 + layer))
+    assert cache.max_layer_seq_len == 6
+    cache.rewind(mark)
+    assert [cache.rows(i) for i in range(3)] == [2, 2, 2]
+    assert torch.equal(cache.attended(2)[0][0], k1)
+    k3, v3 = _rows(1, 20)
+    cache.write_rows(2, k3, v3)
+    assert torch.equal(cache.attended(2)[1][0], torch.cat((v1, v3), dim=1))
+    with pytest.raises(ValueError):
+        cache.rewind((5, 5, 5))  # not an earlier state
+    with pytest.raises(ValueError):
+        cache.rewind((1, 1))
 
 
-def test_storage_views_of_an_arena_entry():
-    """Key / value caches are views of one [L, 2, B, n_kv, S, d] tensor: a
-    write through the manager lands in the storage, and layer_tensors gives
-    the contiguous [n_kv, S, d] block the attention kernel addresses."""
-    layout = _layout()
-    storage = torch.zeros((3, 2, 1, 2, 10, 8), dtype=torch.bfloat16)
-    cache = StaticKVBlockManager(layout, storage)
-    k, v = _states(3, 30)
-    cache.append(2, k, v)
-    assert torch.equal(storage[2, 0, 0, :, :3], k[0]) and torch.equal(storage[2, 1, 0, :, :3], v[0])
+def test_works_in_place_on_an_arena_region():
+    """The cache over a [L, 2, 1, n_kv, S, d] arena entry: writes land in the
+    region, layer_tensors are its contiguous [n_kv, S, d] blocks, and the
+    reference-shaped key_cache / value_cache views see the same memory."""
+    region = torch.zeros((3, 2, 1, 2, 10, 8), dtype=torch.bfloat16)
+    cache = ArenaKVCache(3, 2, 8, 10, storage=region)
+    k, v = _rows(3, 30)
+    cache.write_rows(2, k, v)
+    assert torch.equal(region[2, 0, 0, :, :3], k) and torch.equal(region[2, 1, 0, :, :3], v)
     kl, vl = cache.layer_tensors(2)
     assert kl.shape == (2, 10, 8) and kl.is_contiguous() and vl.is_contiguous()
-    assert kl.data_ptr() == storage[2, 0, 0].data_ptr() and vl.data_ptr() == storage[2, 1, 0].data_ptr()
-    kl[:, 3] = 1.0  # what the kernel's append does, then the cursor moves
+    assert kl.data_ptr() == region[2, 0, 0].data_ptr() and vl.data_ptr() == region[2, 1, 0].data_ptr()
+    assert cache.key_cache.shape == (3, 1, 2, 10, 8) and cache.key_cache.data_ptr() == region.data_ptr()
+    kl[:, 3] = 1.0  # what the decode kernel's append does; then the cursor moves
     cache.advance(2, 1)
-    assert torch.equal(cache.get(2)[0][0, :, 3], torch.ones(2, 8, dtype=torch.bfloat16))
+    assert torch.equal(cache.attended(2)[0][0, :, 3], torch.ones(2, 8, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
-        StaticKVBlockManager(layout, torch.zeros((3, 2, 1, 2, 9, 8), dtype=torch.bfloat16))
+        ArenaKVCache(3, 2, 8, 10, storage=torch.zeros((3, 2, 1, 2, 9, 8), dtype=torch.bfloat16))
     with pytest.raises(ValueError):
-        StaticKVBlockManager(layout, torch.zeros((3, 2, 1, 2, 10, 8), dtype=torch.float32))
+        ArenaKVCache(3, 2, 8, 10, storage=torch.zeros((3, 2, 2, 2, 10, 8), dtype=torch.bfloat16))
 
 
-def test_layer_tensors_serve_batch_one_only():
-    cache = StaticKVBlockManager(_layout(batch_size=2))
-    with pytest.raises(ValueError, match="batch 1"):
-        cache.layer_tensors(0)
+def test_dispatch_reads_the_cache_it_advances():
+    """dispatch's cache accessors on this cache: the layer blocks and the
+    cursor, then one row counted."""
+    cache = _cache()
+    cache.write_rows(1, *_rows(4, 40))
+    k, v, pos = dispatch._static_cache_layer(cache, 1)
+    assert pos == 4 and k.data_ptr() == cache.layer_tensors(1)[0].data_ptr()
+    dispatch._advance_cache(cache, 1)
+    assert cache.rows(1) == 5

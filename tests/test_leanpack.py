@@ -87,6 +87,50 @@ def test_materialize_round_trips_every_tensor(tiny_pack):
     assert runtime.config.num_key_value_heads == 2 and runtime.layers[0].attention.num_key_value_groups == 2
 
 
+def _copy_pack(src, dst, edit):
+    """A copy of the pack at dst whose manifest payload went through edit()."""
+    import shutil
+
+    shutil.copytree(src, dst)
+    payload = json.loads((dst / "manifest.json").read_text())
+    edit(payload)
+    (dst / "manifest.json").write_text(json.dumps(payload))
+    return dst
+
+
+def test_loader_refuses_a_pack_missing_a_planned_weight(tiny_pack, tmp_path):
+    """A planned weight with no tensor in the pack would leave uninitialised
+    arena bytes under the runtime: the loader raises instead."""
+    _, out, _ = tiny_pack
+
+    def drop(payload):
+        payload["tensors"] = [t for t in payload["tensors"] if t["name"] != "layers.1.mlp.down_proj.weight"]
+
+    bad = _copy_pack(out, tmp_path / "truncated", drop)
+    with pytest.raises(ValueError, match="no tensor for 1 planned"):
+        materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
+
+
+def test_loader_refuses_a_mislabelled_layout(tiny_pack, tmp_path):
+    """A gate_up stored as plain mfma16x32 (or a packed weight labelled
+    row-major) has the right byte count but the wrong tile order."""
+    _, out, _ = tiny_pack
+
+    def relabel(name, layout):
+        def edit(payload):
+            for t in payload["tensors"]:
+                if t["name"] == name:
+                    t["layout"] = layout
+        return edit
+
+    bad = _copy_pack(out, tmp_path / "gateup", relabel("layers.0.mlp.gate_up_proj.weight", "mfma16x32"))
+    with pytest.raises(ValueError, match="plan needs 'mfma16x32_gateup'"):
+        materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
+    bad = _copy_pack(out, tmp_path / "rowmajor", relabel("layers.0.attention.o_proj.weight", "rowmajor"))
+    with pytest.raises(ValueError, match="plan needs 'mfma16x32'"):
+        materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
+
+
 @pytest.mark.gpu
 def test_real_shape_layer_from_pack_runs_the_dispatch_path(gpu, tmp_path):
     from leanstack_amd import dispatch

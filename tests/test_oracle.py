@@ -327,3 +327,169 @@ def test_decode_attention_appends_one_row():
     kc_far[:, pos + 1:] = 100.0
     out_far, _, _ = decode_attention(qkv, n_q, n_kv, d, qn, kn, 1e-6, cos, sin, kc_far, vc, pos, d ** -0.5)
     assert torch.equal(out, out_far)
+
+
+# ---------------------------------------------------------------- composite functions
+#
+# The oracle's compositions (post-attention MLP, MLP forward, q/k heads,
+# decode layer) against brute's float64 restatements with the same bf16
+# rounding points.  Each check also runs the float64 chain with a plausible
+# mistake -- a residual joined at the wrong point, a norm on the wrong
+# tensor, swapped q/k norm weights, a wrong kv-head mapping, the new row left
+# out of attention -- and requires that the oracle does NOT match it, so the
+# check is known to catch that mistake.
+
+from oracle import attention as ref_attn  # noqa: E402
+
+
+def _f64(t: torch.Tensor) -> np.ndarray:
+    return brute.bf16_bits_to_f64(bits(t)).reshape(tuple(t.shape))
+
+
+def _agreement(got: np.ndarray, want: np.ndarray) -> tuple[float, float]:
+    """(fraction of bit-equal values, max |got - want| / max |want|)."""
+    return float(np.mean(got == want)), float(np.abs(got - want).max() / np.abs(want).max())
+
+
+def _matches(got, want) -> bool:
+    exact, rel = _agreement(got, want)
+    return exact >= 0.98 and rel <= 1e-2
+
+
+def _differs(got, want) -> bool:
+    exact, rel = _agreement(got, want)
+    return exact < 0.5 and rel > 3e-2
+
+
+class _Rand:
+    def __init__(self, seed):
+        self.rng = np.random.default_rng(seed)
+
+    def __call__(self, *shape, scale=1.0, mean=0.0):
+        return _bf(mean + self.rng.standard_normal(shape) * scale)
+
+
+def test_post_attention_mlp_is_pinned():
+    """_semantic_post_attention_mlp_eager (qwen_explicit.py:809-831):
+    h = residual + o(attn), then h + MLP(rmsnorm(h))."""
+    r = _Rand(21)
+    h_dim, q_dim, inter, t = 64, 96, 80, 3
+    attn, res = r(t, q_dim), r(t, h_dim)
+    o_w, ln = r(h_dim, q_dim, scale=0.1), r(h_dim, scale=0.2, mean=1.0)
+    gu, dn = r(2 * inter, h_dim, scale=0.15), r(h_dim, inter, scale=0.15)
+    got = _f64(ref.post_attention_mlp(attn, res, o_w, ln, gu, inter, dn, 1e-6))
+    A, R, O, L, GU, DN = map(_f64, (attn, res, o_w, ln, gu, dn))
+    assert _matches(got, brute.post_attention_mlp64(A, R, O, L, GU, inter, DN, 1e-6))
+    h = brute.round_bf16(R + brute.proj64(A, O))
+    mlp = lambda x: brute.mlp_forward64(x, GU, inter, DN)  # noqa: E731
+    mistakes = {
+        "residual joins before o_proj's output": brute.round_bf16(R + mlp(brute.rmsnorm64(h, L, 1e-6))),
+        "norm of the residual, not of h": brute.round_bf16(h + mlp(brute.rmsnorm64(R, L, 1e-6))),
+        "norm of o_proj's output": brute.round_bf16(h + mlp(brute.rmsnorm64(brute.proj64(A, O), L, 1e-6))),
+        "no norm": brute.round_bf16(h + mlp(h)),
+        "no final residual": mlp(brute.rmsnorm64(h, L, 1e-6)),
+    }
+    for what, wrong in mistakes.items():
+        assert _differs(got, wrong), what
+
+
+def test_mlp_forward_is_pinned():
+    """semantic_qwen_mlp_forward (qwen_explicit.py:1201-1208): down(SiLU(gate) * up)."""
+    r = _Rand(22)
+    h_dim, inter, t = 64, 80, 4
+    x, gu, dn = r(t, h_dim), r(2 * inter, h_dim, scale=0.15), r(h_dim, inter, scale=0.15)
+    got = _f64(ref.mlp_forward(x, gu, inter, dn))
+    X, GU, DN = map(_f64, (x, gu, dn))
+    assert _matches(got, brute.mlp_forward64(X, GU, inter, DN))
+    g = brute.proj64(X, GU)
+    swapped = np.concatenate((g[:, inter:], g[:, :inter]), axis=1)
+    mistakes = {
+        "SiLU on the up half": brute.proj64(brute.silu_mul64(swapped, inter), DN),
+        "no SiLU": brute.proj64(brute.round_bf16(g[:, :inter] * g[:, inter:]), DN),
+        "down of the gate half alone": brute.proj64(g[:, :inter], DN),
+    }
+    for what, wrong in mistakes.items():
+        assert _differs(got, wrong), what
+
+
+def _qk_case(seed):
+    r = _Rand(seed)
+    n_q, n_kv, d = 4, 2, 16
+    qkv = r((n_q + 2 * n_kv) * d, scale=2.0)
+    qn, kn = r(d, scale=0.3, mean=1.0), r(d, scale=0.3, mean=1.0)
+    ang = r.rng.uniform(0.3, 6.0, d // 2)
+    return n_q, n_kv, d, qkv, qn, kn, _bf(np.cos(ang)), _bf(np.sin(ang))
+
+
+def test_qk_heads_vector_is_pinned():
+    """The tail of _semantic_attention_qkv_vector_eager (qwen_explicit.py:
+    788-806): split [q | k | v], q heads normalised with q_norm_weight and k
+    heads with k_norm_weight, each over head_dim, then RoPE."""
+    n_q, n_kv, d, qkv, qn, kn, cos, sin = _qk_case(23)
+    q, k, v = ref_attn.qk_heads_vector(qkv, n_q, n_kv, d, qn, kn, 1e-6, cos, sin)
+    got_q, got_k, got_v = _f64(q).reshape(n_q, d), _f64(k).reshape(n_kv, d), _f64(v).reshape(n_kv, d)
+    QKV, QN, KN, C, S = map(_f64, (qkv, qn, kn, cos, sin))
+    want_q, want_k, want_v = brute.qk_heads64(QKV, n_q, n_kv, d, QN, KN, 1e-6, C, S)
+    assert _matches(got_q, want_q) and _matches(got_k, want_k) and np.array_equal(got_v, want_v)
+    swapped_q, swapped_k, _ = brute.qk_heads64(QKV, n_q, n_kv, d, KN, QN, 1e-6, C, S)
+    assert _differs(got_q, swapped_q) and _differs(got_k, swapped_k), "q/k norm weights swapped"
+    qs = QKV[: n_q * d]
+    whole = brute.rope64(brute.round_bf16(qs * QN.repeat(n_q) / np.sqrt((qs * qs).mean() + 1e-6)).reshape(n_q, d),
+                         C, S)
+    assert _differs(got_q, whole), "q normalised over all heads at once"
+    unrotated_q, _, _ = brute.qk_heads64(QKV, n_q, n_kv, d, QN, KN, 1e-6, np.ones_like(C), np.zeros_like(S))
+    assert _differs(got_q, unrotated_q), "RoPE left out"
+    assert _differs(got_q, brute.qk_heads64(QKV, n_q, n_kv, d, QN, KN, 1e-6, C, -S)[0]), "RoPE sign flipped"
+
+
+def _layer64_with(mistake, hidden, in_ln, qkv_w, n_q, n_kv, d, qn, kn, cos, sin, kc, vc, pos, scale, o_w, post_ln,
+                  gu, inter, dn, eps):
+    """brute.decode_layer64's chain with one named mistake (None: none)."""
+    if mistake == "q/k norms swapped":
+        qn, kn = kn, qn
+    x = hidden if mistake != "no input norm" else None
+    qkv = brute.proj64(brute.rmsnorm64(hidden, in_ln, eps) if x is not None else hidden, qkv_w)
+    q, k, v = brute.qk_heads64(qkv, n_q, n_kv, d, qn, kn, eps, cos, sin)
+    kc, vc = kc.copy(), vc.copy()
+    kc[:, pos], vc[:, pos] = k, v
+    rows = pos if mistake == "new row not attended" else pos + 1
+    if mistake == "kv head h % n_kv":
+        q = q.reshape(n_q // n_kv, n_kv, d).transpose(1, 0, 2).reshape(n_q, d)
+        a = brute.attention64(q, kc[:, :rows], vc[:, :rows], scale)
+        attn = a.reshape(n_kv, n_q // n_kv, d).transpose(1, 0, 2).reshape(-1)
+    else:
+        attn = brute.attention64(q, kc[:, :rows], vc[:, :rows], scale).reshape(-1)
+    h = brute.round_bf16(hidden + brute.proj64(attn, o_w))
+    normed = brute.rmsnorm64(hidden if mistake == "post norm of the layer input" else h, post_ln, eps)
+    base = hidden if mistake == "final residual is the layer input" else h
+    return brute.round_bf16(base + brute.mlp_forward64(normed, gu, inter, dn)), kc, vc
+
+
+def test_decode_layer_is_pinned():
+    """semantic_qwen_decode_layer_forward (qwen_explicit.py:1247-1272) with a
+    filled cache: the output and the appended cache row against brute's
+    float64 chain, and five plausible mistakes that the check rejects."""
+    r = _Rand(24)
+    h_dim, n_q, n_kv, d, inter, s_max, pos = 64, 4, 2, 16, 80, 8, 5
+    hidden = r(h_dim, scale=2.0)
+    in_ln, post_ln = r(h_dim, scale=0.2, mean=1.0), r(h_dim, scale=0.2, mean=1.0)
+    qkv_w = r((n_q + 2 * n_kv) * d, h_dim, scale=0.2)
+    qn, kn = r(d, scale=0.3, mean=1.0), r(d, scale=0.3, mean=1.0)
+    o_w, gu, dn = r(h_dim, n_q * d, scale=0.15), r(2 * inter, h_dim, scale=0.15), r(h_dim, inter, scale=0.15)
+    kc, vc = r(n_kv, s_max, d, scale=2.0), r(n_kv, s_max, d)
+    ang = r.rng.uniform(0.3, 6.0, d // 2)
+    cos, sin = _bf(np.cos(ang)), _bf(np.sin(ang))
+    scale = d ** -0.5
+    out, kc_new, vc_new = ref_attn.decode_layer(hidden, in_ln, qkv_w, n_q, n_kv, d, qn, kn, cos, sin, kc, vc, pos,
+                                                scale, o_w, post_ln, gu, inter, dn, 1e-6)
+    args = [_f64(hidden), _f64(in_ln), _f64(qkv_w), n_q, n_kv, d, _f64(qn), _f64(kn), _f64(cos), _f64(sin), _f64(kc),
+            _f64(vc), pos, scale, _f64(o_w), _f64(post_ln), _f64(gu), inter, _f64(dn), 1e-6]
+    want, want_kc, want_vc = brute.decode_layer64(*args)
+    got = _f64(out)
+    assert _matches(got, want)
+    assert _matches(_f64(kc_new)[:, pos], want_kc[:, pos]) and np.array_equal(_f64(vc_new), want_vc)
+    assert np.array_equal(_f64(kc_new)[:, :pos], _f64(kc)[:, :pos])  # only row pos changes
+    assert np.array_equal(_layer64_with(None, *args)[0], want)
+    for mistake in ("q/k norms swapped", "new row not attended", "kv head h % n_kv", "post norm of the layer input",
+                    "final residual is the layer input", "no input norm"):
+        assert _differs(got, _layer64_with(mistake, *args)[0]), mistake
