@@ -232,6 +232,20 @@ int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, 
                                     float* logits_opt, int logits_mode, long long* out_idx,
                                     void* workspace, size_t ws_bytes, void* hip_stream);
 
+/* lsk_lm_head_argmax_bf16 without the workspace: the argmax partials live in
+ * a static device array of the library (1 MiB per device), so the call
+ * allocates nothing.  No counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Limit: M * (V / 32) * 8 bytes of
+ * partials must fit in 1 MiB (every M <= 16 at V = 151936); larger calls
+ * return LSK_ERR_INVALID before anything touches the GPU.  All calls on one
+ * device share the array: calls that overlap in time on a device (streams not
+ * ordered with each other) race; stream-ordered calls do not. */
+int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_id, int V, int K,
+                                    const void* x, int M, int ldx,
+                                    float* logits_opt, int logits_mode, long long* out_idx,
+                                    void* hip_stream);
+
 /* ------------------------------------------------------------------------
  * Stack programs: a whole decode / verify step of projections in ONE launch.
  *

@@ -82,6 +82,10 @@ _SIGNATURES: dict[str, tuple[type | None, list]] = {
         [_c_void, _c_int, _c_int, _c_int, _c_void, _c_int, _c_int, _c_void, ctypes.c_float, _c_void, _c_int, _c_void,
          _c_void, _c_size, _c_void],
     ),
+    "lsk_lm_head_argmax_noalloc_bf16": (
+        _c_int,
+        [_c_void, _c_int, _c_int, _c_int, _c_void, _c_int, _c_int, _c_void, _c_int, _c_void, _c_void],
+    ),
 }
 
 class Projection(ctypes.Structure):

@@ -313,10 +313,10 @@ int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_di
 
 namespace {
 
-// Checks and launch shared by the plain and the RMSNorm lm_head entry points.
-int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
-                   const void* norm_weight, float eps, float* logits_opt, int logits_mode, long long* out_idx,
-                   void* workspace, size_t ws_bytes, void* hip_stream) {
+// Every lm_head argument rule but the workspace's (shared by the lm_head
+// entry points).
+int check_lm_head(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                  const float* logits_opt, int logits_mode, const long long* out_idx) {
   if (layout_id != LSK_LAYOUT_MFMA16X32)
     return fail(LSK_ERR_LAYOUT, "lm_head needs layout %d, got %d", LSK_LAYOUT_MFMA16X32, layout_id);
   if (int st = check_shape(layout_id, V, K)) return st;
@@ -332,6 +332,14 @@ int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void
   if (logits_opt != nullptr && !aligned(logits_opt, 16))
     return fail(LSK_ERR_INVALID, "logits buffer must be 16-byte aligned");
   if (!aligned(out_idx, 8)) return fail(LSK_ERR_INVALID, "out_idx must be 8-byte aligned");
+  return LSK_OK;
+}
+
+// Checks and launch shared by the plain and the RMSNorm lm_head entry points.
+int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                   const void* norm_weight, float eps, float* logits_opt, int logits_mode, long long* out_idx,
+                   void* workspace, size_t ws_bytes, void* hip_stream) {
+  if (int st = check_lm_head(w_packed, layout_id, V, K, x, M, ldx, logits_opt, logits_mode, out_idx)) return st;
   const size_t need = lsk_workspace_bytes(LSK_OP_LM_HEAD_ARGMAX, M, V, K);
   if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 8))
     return fail(LSK_ERR_WORKSPACE, "lm_head workspace needs %zu bytes, got %zu", need, workspace ? ws_bytes : 0);
@@ -343,6 +351,24 @@ int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void
 }
 
 }  // namespace
+
+}  // extern "C"
+
+namespace lsk {
+
+int check_lm_head_call(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                       const float* logits_opt, int logits_mode, const long long* out_idx) {
+  g_last_error.clear();
+  return check_lm_head(w_packed, layout_id, V, K, x, M, ldx, logits_opt, logits_mode, out_idx);
+}
+
+int fail_call(int status, const char* message) { return fail(status, "%s", message); }
+
+int fail_hip_call(hipError_t err, const char* what) { return hip_fail(err, what); }
+
+}  // namespace lsk
+
+extern "C" {
 
 int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
                             float* logits_opt, int logits_mode, long long* out_idx, void* workspace,

@@ -147,6 +147,14 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
                                  float* logits, int logits_bf16, long long* out_idx,
                                  ArgmaxPartial* partials, const void* norm_w, float eps, hipStream_t stream);
 
+// lm_head argument checks of the C ABI (everything but the workspace),
+// clearing and then recording lsk_last_error's message; and the recorders
+// themselves, for entry points defined outside abi.cpp.
+int check_lm_head_call(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
+                       const float* logits_opt, int logits_mode, const long long* out_idx);
+int fail_call(int status, const char* message);
+int fail_hip_call(hipError_t err, const char* what);
+
 // Workspace bytes the split-K prefill path needs on `device` for this shape
 // (0 when the shape does not take it).  Sets *status to a HIP error if the
 // device query fails.

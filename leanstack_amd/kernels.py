@@ -338,6 +338,33 @@ def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: i
     return out
 
 
+def lm_head_argmax_noalloc(hidden: torch.Tensor, weight: PackedWeight, out: torch.Tensor, *,
+                           logits_mode: int = _lib.LOGITS_FP32, logits_out: torch.Tensor | None = None) -> torch.Tensor:
+    """lm_head_argmax with no allocation anywhere on the call: the argmax
+    partials use the library's static device scratch
+    (lsk_lm_head_argmax_noalloc_bf16), `out` (int64, at least M values) is
+    the caller's, and `hidden` must already be contiguous [M, K] bf16 rows.
+    Usable under HIP graph capture; calls on one device that are not
+    stream-ordered with each other race on the scratch."""
+    if not isinstance(weight, PackedWeight) or weight.layout != _lib.LAYOUT_MFMA16X32:
+        raise ValueError("lm_head weight must be a PackedWeight in the mfma16x32 layout")
+    if hidden.dtype != torch.bfloat16 or hidden.shape[-1] != weight.k or not hidden.is_contiguous():
+        raise ValueError(f"hidden must be contiguous bfloat16 [M, {weight.k}] rows")
+    m = hidden.numel() // weight.k
+    if out.dtype != torch.long or out.numel() < m or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous int64 tensor of at least {m} values")
+    if logits_out is not None and (logits_out.dtype != torch.float32 or logits_out.numel() != m * weight.n
+                                   or not logits_out.is_contiguous()):
+        raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{weight.n}")
+    for t, what in ((hidden, "hidden"), (weight.data, "weight"), (out, "out")):
+        _require_device(t, what)
+    status = _lib.load().lsk_lm_head_argmax_noalloc_bf16(
+        weight.data.data_ptr(), weight.layout, weight.n, weight.k, hidden.data_ptr(), m, weight.k,
+        logits_out.data_ptr() if logits_out is not None else None, logits_mode, out.data_ptr(), stream_handle())
+    _lib.check(status, "lsk_lm_head_argmax_noalloc_bf16")
+    return out
+
+
 class StackStep:
     """A prepared stack program: many projections at the same M in one
     persistent launch (lsk_stack_prepare / lsk_stack_run).

@@ -263,3 +263,23 @@ def test_launch_next_refuses_a_bad_token_buffer():
                 torch.zeros(0, dtype=torch.long)):
         with pytest.raises(ValueError, match="tokens_out"):
             step.launch_next(emb, bad)
+
+
+def test_noalloc_lm_head_rejects_before_launch():
+    """The allocation-free head refuses calls whose partials exceed its
+    static scratch (M * V / 32 * 8 bytes > 1 MiB) and the usual bad
+    arguments, before touching the GPU."""
+    lib = _lib.load()
+
+    def call(**over):
+        a = dict(w=FAKE, layout=1, v=151936, k=2560, x=FAKE, m=1, ldx=2560, logits=None, mode=0, out=FAKE)
+        a.update(over)
+        return lib.lsk_lm_head_argmax_noalloc_bf16(a["w"], a["layout"], a["v"], a["k"], a["x"], a["m"], a["ldx"],
+                                                   a["logits"], a["mode"], a["out"], None)
+
+    st = call(m=16, v=1 << 19)  # 16 rows x 16384 partials x 8 B = 2 MiB
+    assert st == _lib.ERR_INVALID and "static scratch" in _lib.last_error()
+    assert call(m=17) == _lib.ERR_INVALID
+    assert call(layout=2) == _lib.ERR_LAYOUT
+    assert call(mode=7) == _lib.ERR_INVALID
+    assert call(out=FAKE + 4) == _lib.ERR_INVALID
