@@ -1,4 +1,6 @@
-// extern "C" surface of libleanstack_amd.so (declared in include/leanstack_amd.h).
+// extern "C" surface of libleanstack_amd.so (declared in include/leanstack_amd.h):
+// the entry points that launch kernels or touch device memory.  The packers,
+// the argument rules and lsk_last_error() are in host_rules.cpp.
 //
 // Every entry point validates its arguments before touching the GPU, records
 // a message for lsk_last_error() on failure and returns a negative status;
@@ -23,83 +25,12 @@
 
 namespace {
 
-thread_local std::string g_last_error;
-
-int fail(int status, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
-  g_last_error = buf;
-  return status;
-}
+using lsk::aligned;
+using lsk::check_shape;
+using lsk::fail;
 
 int hip_fail(hipError_t err, const char* what) {
   return fail(LSK_ERR_HIP, "%s: %s (%s)", what, hipGetErrorName(err), hipGetErrorString(err));
-}
-
-bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-
-bool packed_layout(int layout_id) {
-  return layout_id == LSK_LAYOUT_MFMA16X32 || layout_id == LSK_LAYOUT_MFMA16X32_GATEUP;
-}
-
-// Shape rules of the packed layouts: whole 16x32 tiles, and whole gate/up
-// row-block pairs for the interleaved layout.
-int check_shape(int layout_id, int N, int K) {
-  if (!packed_layout(layout_id)) return fail(LSK_ERR_LAYOUT, "unsupported weight layout id %d", layout_id);
-  if (N <= 0 || K <= 0) return fail(LSK_ERR_INVALID, "N=%d and K=%d must be positive", N, K);
-  if (N % lsk::kTileRows != 0) return fail(LSK_ERR_INVALID, "N=%d must be divisible by %d", N, lsk::kTileRows);
-  if (K % lsk::kTileK != 0) return fail(LSK_ERR_INVALID, "K=%d must be divisible by %d", K, lsk::kTileK);
-  if (layout_id == LSK_LAYOUT_MFMA16X32_GATEUP && N % (2 * lsk::kTileRows) != 0)
-    return fail(LSK_ERR_INVALID, "fused gate_up N=%d must be divisible by %d", N, 2 * lsk::kTileRows);
-  return LSK_OK;
-}
-
-// Row of the row-major source matrix stored in packed row `pr`.
-inline int source_row(int layout_id, int N, int pr) {
-  if (layout_id != LSK_LAYOUT_MFMA16X32_GATEUP) return pr;
-  const int half = N / 2;
-  const int pair = pr / (2 * lsk::kTileRows);
-  const int within = pr % (2 * lsk::kTileRows);
-  return within < lsk::kTileRows ? pair * lsk::kTileRows + within
-                                 : half + pair * lsk::kTileRows + (within - lsk::kTileRows);
-}
-
-// Byte offset (in 16-byte units) of W[packed row pr][k8 * 8 .. +8] in the tiles.
-inline size_t packed_unit(int K, int pr, int k8) {
-  const int KT = K / lsk::kTileK;
-  const int rb = pr / lsk::kTileRows;
-  const int r = pr % lsk::kTileRows;
-  const int kt = k8 / 4;
-  const int gq = k8 % 4;
-  return ((size_t)rb * KT + kt) * 64 + (size_t)gq * 16 + r;
-}
-
-// Argument rules shared by the projection entry points (see lsk_linear_bf16).
-int check_linear_args(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx,
-                      const void* y, int ldy, int epilogue, const void* residual, int ldr) {
-  if (int st = check_shape(layout_id, N, K)) return st;
-  if (epilogue != LSK_EPI_NONE && epilogue != LSK_EPI_SILU_MUL && epilogue != LSK_EPI_RESIDUAL_ADD)
-    return fail(LSK_ERR_INVALID, "unknown epilogue %d", epilogue);
-  if ((epilogue == LSK_EPI_SILU_MUL) != (layout_id == LSK_LAYOUT_MFMA16X32_GATEUP))
-    return fail(LSK_ERR_INVALID, "the SiLU*up epilogue requires the interleaved gate_up layout and vice versa");
-  if (M < 1) return fail(LSK_ERR_INVALID, "M=%d must be >= 1", M);
-  if (w_packed == nullptr || x == nullptr || y == nullptr) return fail(LSK_ERR_INVALID, "null device pointer");
-  if (!aligned(w_packed, 16)) return fail(LSK_ERR_INVALID, "packed weights must be 16-byte aligned");
-  if (ldx < K || ldx % 8 != 0 || !aligned(x, 16))
-    return fail(LSK_ERR_INVALID, "x needs ldx >= K, ldx %% 8 == 0 and 16-byte alignment (ldx=%d, K=%d)", ldx, K);
-  const int n_out = epilogue == LSK_EPI_SILU_MUL ? N / 2 : N;
-  if (ldy < n_out || ldy % 4 != 0 || !aligned(y, 8))
-    return fail(LSK_ERR_INVALID, "y needs ldy >= %d, ldy %% 4 == 0 and 8-byte alignment (ldy=%d)", n_out, ldy);
-  if (epilogue == LSK_EPI_RESIDUAL_ADD) {
-    if (residual == nullptr || ldr < N || !aligned(residual, 2))
-      return fail(LSK_ERR_INVALID, "residual add needs a residual [M][N] with ldr >= N (ldr=%d)", ldr);
-  } else if (residual != nullptr) {
-    return fail(LSK_ERR_INVALID, "residual given without the residual-add epilogue");
-  }
-  return LSK_OK;
 }
 
 }  // namespace
@@ -122,13 +53,6 @@ extern "C" {
 
 int lsk_abi_version(void) { return LSK_ABI_VERSION; }
 
-const char* lsk_last_error(void) { return g_last_error.c_str(); }
-
-size_t lsk_packed_bytes(int layout_id, int N, int K) {
-  if (check_shape(layout_id, N, K) != LSK_OK) return 0;
-  return (size_t)N * (size_t)K * 2;
-}
-
 size_t lsk_workspace_bytes(int op, int M, int N, int K) {
   if (op == LSK_OP_LINEAR) {
     if (M <= lsk::kDecodeMaxM || N <= 0 || K <= 0) return 0;
@@ -145,39 +69,11 @@ size_t lsk_workspace_bytes(int op, int M, int N, int K) {
   return 0;
 }
 
-int lsk_pack_bf16(const void* w_rowmajor_host, int N, int K, int layout_id, void* out_host) {
-  g_last_error.clear();
-  if (int st = check_shape(layout_id, N, K)) return st;
-  if (w_rowmajor_host == nullptr || out_host == nullptr) return fail(LSK_ERR_INVALID, "null buffer");
-  const auto* src = static_cast<const unsigned char*>(w_rowmajor_host);
-  auto* dst = static_cast<unsigned char*>(out_host);
-  const int k8s = K / 8;
-  for (int pr = 0; pr < N; ++pr) {
-    const unsigned char* row = src + (size_t)source_row(layout_id, N, pr) * K * 2;
-    for (int k8 = 0; k8 < k8s; ++k8) std::memcpy(dst + packed_unit(K, pr, k8) * 16, row + (size_t)k8 * 16, 16);
-  }
-  return LSK_OK;
-}
-
-int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* out_rowmajor_host) {
-  g_last_error.clear();
-  if (int st = check_shape(layout_id, N, K)) return st;
-  if (packed_host == nullptr || out_rowmajor_host == nullptr) return fail(LSK_ERR_INVALID, "null buffer");
-  const auto* src = static_cast<const unsigned char*>(packed_host);
-  auto* dst = static_cast<unsigned char*>(out_rowmajor_host);
-  const int k8s = K / 8;
-  for (int pr = 0; pr < N; ++pr) {
-    unsigned char* row = dst + (size_t)source_row(layout_id, N, pr) * K * 2;
-    for (int k8 = 0; k8 < k8s; ++k8) std::memcpy(row + (size_t)k8 * 16, src + packed_unit(K, pr, k8) * 16, 16);
-  }
-  return LSK_OK;
-}
-
 int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx, void* y,
                     int ldy, int epilogue, const void* residual, int ldr, void* workspace, size_t ws_bytes,
                     void* hip_stream) {
-  g_last_error.clear();
-  if (int st = check_linear_args(w_packed, layout_id, N, K, x, M, ldx, y, ldy, epilogue, residual, ldr)) return st;
+  lsk::clear_error();
+  if (int st = lsk::check_linear_args(w_packed, layout_id, N, K, x, M, ldx, y, ldy, epilogue, residual, ldr)) return st;
   auto stream = static_cast<hipStream_t>(hip_stream);
   const auto epi = static_cast<lsk::Epilogue>(epilogue);
   hipError_t err;
@@ -214,8 +110,8 @@ int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const voi
 int lsk_rmsnorm_linear_bf16(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx,
                             const void* norm_weight, float eps, void* y, int ldy, int epilogue,
                             const void* residual, int ldr, void* hip_stream) {
-  g_last_error.clear();
-  if (int st = check_linear_args(w_packed, layout_id, N, K, x, M, ldx, y, ldy, epilogue, residual, ldr)) return st;
+  lsk::clear_error();
+  if (int st = lsk::check_linear_args(w_packed, layout_id, N, K, x, M, ldx, y, ldy, epilogue, residual, ldr)) return st;
   if (M > lsk::kDecodeMaxM)
     return fail(LSK_ERR_INVALID, "the fused RMSNorm projection takes M=1..%d rows (M=%d)", lsk::kDecodeMaxM, M);
   if (norm_weight == nullptr || !aligned(norm_weight, 16))
@@ -238,31 +134,6 @@ size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_se
 
 namespace {
 
-// Checks shared by both attention entry points (everything but pos).
-int check_attention_args(const void* qkv, int n_q, int n_kv, int head_dim, const void* q_norm_weight,
-                         const void* k_norm_weight, float eps, const void* cos, const void* sin, void* k_cache,
-                         void* v_cache, int max_seq_len, float scale, void* out) {
-  if (head_dim != lsk::kAttnHeadDim)
-    return fail(LSK_ERR_INVALID, "head_dim=%d: the attention kernel is built for %d", head_dim, lsk::kAttnHeadDim);
-  if (n_kv < 1 || n_kv > lsk::kAttnMaxKvHeads || n_q < n_kv || n_q % n_kv != 0 ||
-      !lsk::attention_group_supported(n_q / n_kv))
-    return fail(LSK_ERR_INVALID, "n_q=%d, n_kv=%d: n_kv must be 1..%d and n_q 1, 2, 4 or 8 times n_kv", n_q, n_kv,
-                lsk::kAttnMaxKvHeads);
-  if (qkv == nullptr || q_norm_weight == nullptr || k_norm_weight == nullptr || cos == nullptr || sin == nullptr ||
-      k_cache == nullptr || v_cache == nullptr || out == nullptr)
-    return fail(LSK_ERR_INVALID, "null device pointer");
-  if (!aligned(qkv, 2) || !aligned(q_norm_weight, 2) || !aligned(k_norm_weight, 2) || !aligned(cos, 2) ||
-      !aligned(sin, 2) || !aligned(out, 2))
-    return fail(LSK_ERR_INVALID, "bf16 arguments must be 2-byte aligned");
-  if (!aligned(k_cache, 16) || !aligned(v_cache, 16))
-    return fail(LSK_ERR_INVALID, "the key and value caches must be 16-byte aligned");
-  if (max_seq_len < 1 || max_seq_len > lsk::kAttnMaxRows)
-    return fail(LSK_ERR_INVALID, "max_seq_len=%d: need 1 <= max_seq_len <= %d", max_seq_len, lsk::kAttnMaxRows);
-  if (!std::isfinite(eps) || eps < 0.f) return fail(LSK_ERR_INVALID, "eps=%g must be finite and >= 0", (double)eps);
-  if (!std::isfinite(scale)) return fail(LSK_ERR_INVALID, "scale must be finite");
-  return LSK_OK;
-}
-
 int check_attention_workspace(int n_q, int n_kv, int max_seq_len, int rows, const void* workspace,
                               size_t ws_bytes) {
   if (rows <= lsk::kAttnMinChunkRows) return LSK_OK;
@@ -279,8 +150,8 @@ int lsk_decode_attention_bf16(const void* qkv, int n_q, int n_kv, int head_dim, 
                               const void* k_norm_weight, float eps, const void* cos, const void* sin, void* k_cache,
                               void* v_cache, int max_seq_len, int pos, float scale, void* out, void* workspace,
                               size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
-  if (int st = check_attention_args(qkv, n_q, n_kv, head_dim, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
+  lsk::clear_error();
+  if (int st = lsk::check_attention_args(qkv, n_q, n_kv, head_dim, q_norm_weight, k_norm_weight, eps, cos, sin, k_cache,
                                     v_cache, max_seq_len, scale, out))
     return st;
   if (pos < 0 || pos >= max_seq_len)
@@ -297,8 +168,8 @@ int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_di
                                  const void* k_norm_weight, float eps, const void* cos_table, const void* sin_table,
                                  void* k_cache, void* v_cache, int max_seq_len, const int* pos_device, float scale,
                                  void* out, void* workspace, size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
-  if (int st = check_attention_args(qkv, n_q, n_kv, head_dim, q_norm_weight, k_norm_weight, eps, cos_table,
+  lsk::clear_error();
+  if (int st = lsk::check_attention_args(qkv, n_q, n_kv, head_dim, q_norm_weight, k_norm_weight, eps, cos_table,
                                     sin_table, k_cache, v_cache, max_seq_len, scale, out))
     return st;
   if (pos_device == nullptr || !aligned(pos_device, 4))
@@ -313,33 +184,11 @@ int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_di
 
 namespace {
 
-// Every lm_head argument rule but the workspace's (shared by the lm_head
-// entry points).
-int check_lm_head(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
-                  const float* logits_opt, int logits_mode, const long long* out_idx) {
-  if (layout_id != LSK_LAYOUT_MFMA16X32)
-    return fail(LSK_ERR_LAYOUT, "lm_head needs layout %d, got %d", LSK_LAYOUT_MFMA16X32, layout_id);
-  if (int st = check_shape(layout_id, V, K)) return st;
-  if (V % (2 * lsk::kTileRows) != 0)
-    return fail(LSK_ERR_INVALID, "vocab size V=%d must be divisible by %d", V, 2 * lsk::kTileRows);
-  if (M < 1 || M > lsk::kDecodeMaxM) return fail(LSK_ERR_INVALID, "M=%d must be in 1..%d", M, lsk::kDecodeMaxM);
-  if (logits_mode != LSK_LOGITS_FP32 && logits_mode != LSK_LOGITS_BF16)
-    return fail(LSK_ERR_INVALID, "unknown logits mode %d", logits_mode);
-  if (w_packed == nullptr || x == nullptr || out_idx == nullptr) return fail(LSK_ERR_INVALID, "null device pointer");
-  if (!aligned(w_packed, 16)) return fail(LSK_ERR_INVALID, "packed weights must be 16-byte aligned");
-  if (ldx < K || ldx % 8 != 0 || !aligned(x, 16))
-    return fail(LSK_ERR_INVALID, "x needs ldx >= K, ldx %% 8 == 0 and 16-byte alignment (ldx=%d, K=%d)", ldx, K);
-  if (logits_opt != nullptr && !aligned(logits_opt, 16))
-    return fail(LSK_ERR_INVALID, "logits buffer must be 16-byte aligned");
-  if (!aligned(out_idx, 8)) return fail(LSK_ERR_INVALID, "out_idx must be 8-byte aligned");
-  return LSK_OK;
-}
-
 // Checks and launch shared by the plain and the RMSNorm lm_head entry points.
 int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
                    const void* norm_weight, float eps, float* logits_opt, int logits_mode, long long* out_idx,
                    void* workspace, size_t ws_bytes, void* hip_stream) {
-  if (int st = check_lm_head(w_packed, layout_id, V, K, x, M, ldx, logits_opt, logits_mode, out_idx)) return st;
+  if (int st = lsk::check_lm_head(w_packed, layout_id, V, K, x, M, ldx, logits_opt, logits_mode, out_idx)) return st;
   const size_t need = lsk_workspace_bytes(LSK_OP_LM_HEAD_ARGMAX, M, V, K);
   if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 8))
     return fail(LSK_ERR_WORKSPACE, "lm_head workspace needs %zu bytes, got %zu", need, workspace ? ws_bytes : 0);
@@ -356,14 +205,6 @@ int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void
 
 namespace lsk {
 
-int check_lm_head_call(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
-                       const float* logits_opt, int logits_mode, const long long* out_idx) {
-  g_last_error.clear();
-  return check_lm_head(w_packed, layout_id, V, K, x, M, ldx, logits_opt, logits_mode, out_idx);
-}
-
-int fail_call(int status, const char* message) { return fail(status, "%s", message); }
-
 int fail_hip_call(hipError_t err, const char* what) { return hip_fail(err, what); }
 
 }  // namespace lsk
@@ -373,7 +214,7 @@ extern "C" {
 int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
                             float* logits_opt, int logits_mode, long long* out_idx, void* workspace,
                             size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
+  lsk::clear_error();
   return lm_head_argmax(w_packed, layout_id, V, K, x, M, ldx, nullptr, 0.f, logits_opt, logits_mode, out_idx,
                         workspace, ws_bytes, hip_stream);
 }
@@ -381,7 +222,7 @@ int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, c
 int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
                                     const void* norm_weight, float eps, float* logits_opt, int logits_mode,
                                     long long* out_idx, void* workspace, size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
+  lsk::clear_error();
   if (K != 80 * lsk::kTileK || M > 8)
     return fail(LSK_ERR_INVALID, "the RMSNorm lm_head serves K=%d and M <= 8 (got K=%d, M=%d)", 80 * lsk::kTileK, K,
                 M);
@@ -440,7 +281,7 @@ size_t lsk_stack_workspace_bytes(int count) {
 }
 
 int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void* program_dev, size_t program_bytes) {
-  g_last_error.clear();
+  lsk::clear_error();
   if (projections == nullptr || count <= 0) return fail(LSK_ERR_INVALID, "empty stack program");
   if (count > lsk::kStackMaxProjections)
     return fail(LSK_ERR_INVALID, "stack program of %d projections (at most %d)", count, lsk::kStackMaxProjections);
@@ -454,7 +295,10 @@ int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void*
   prog->magic = lsk::kStackMagic;
   for (int i = 0; i < count; ++i) {
     const lsk_projection& p = projections[i];
-    if (int st = check_shape(p.layout_id, p.N, p.K)) return fail(st, "projection %d: %s", i, g_last_error.c_str());
+    if (int st = check_shape(p.layout_id, p.N, p.K)) {
+      const std::string why = lsk::error_message();
+      return fail(st, "projection %d: %s", i, why.c_str());
+    }
     const int KT = p.K / lsk::kTileK;
     if (KT % lsk::kStackSegTiles != 0)
       return fail(LSK_ERR_INVALID, "projection %d: K=%d must be a multiple of %d", i, p.K,
@@ -499,7 +343,7 @@ int lsk_stack_prepare(const lsk_projection* projections, int count, int M, void*
 }
 
 int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws_bytes, void* hip_stream) {
-  g_last_error.clear();
+  lsk::clear_error();
   if (program_dev == nullptr || count <= 0) return fail(LSK_ERR_INVALID, "null or empty stack program");
   // A workspace below the one-workgroup size is wrong on any device.
   if (workspace == nullptr || ws_bytes < lsk::kStackWsBytes(count, 1) || !aligned(workspace, 256))
@@ -521,12 +365,12 @@ int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws
 }
 
 int lsk_stack_error(void* workspace, int* error_out) {
-  g_last_error.clear();
+  lsk::clear_error();
   return read_clear_error_word(workspace, lsk::kStackWsError, error_out);
 }
 
 int lsk_linear_error(void* workspace, int* error_out) {
-  g_last_error.clear();
+  lsk::clear_error();
   return read_clear_error_word(workspace, 0, error_out);
 }
 

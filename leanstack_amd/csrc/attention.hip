@@ -525,8 +525,6 @@ size_t attention_workspace_bytes(int n_q, int n_kv, int max_seq_len) {
   return kAttnPartialsOffset + (size_t)n_kv * chunks * partial_slot_bytes(group);
 }
 
-bool attention_group_supported(int group) { return group == 1 || group == 2 || group == 4 || group == 8; }
-
 namespace {
 
 AttnArgs common_args(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w, float eps,

@@ -6,16 +6,10 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "lsk_host.h"
+
 namespace lsk {
 
-// Tile geometry of LSK_LAYOUT_MFMA16X32: 16 rows x 32 K of bf16 = 1024 bytes,
-// one v_mfma_f32_16x16x32_bf16 operand per 64-lane wavefront.
-constexpr int kTileRows = 16;
-constexpr int kTileK = 32;
-constexpr int kTileBytes = kTileRows * kTileK * 2;
-
-// Largest M served by the decode/verify kernel (the MFMA column count).
-constexpr int kDecodeMaxM = 16;
 
 // Prefill GEMM block tile: BN weight rows x BM tokens x BK.
 constexpr int kGemmBN = 128;
@@ -105,16 +99,7 @@ hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void*
 // Workspace: one arrival counter per kv head (kAttnMaxKvHeads words), then
 // from kAttnPartialsOffset one partial slot per (kv head, chunk).
 // Zero-filled before first use; every launch leaves the counters zero.
-constexpr int kAttnHeadDim = 128;
-constexpr int kAttnMinChunkRows = 128;
-constexpr int kAttnMaxChunkRows = 512;
-constexpr int kAttnMaxChunks = 32;
-constexpr int kAttnMaxRows = kAttnMaxChunks * kAttnMaxChunkRows;  // 16384
-constexpr int kAttnMaxKvHeads = 64;
 constexpr size_t kAttnPartialsOffset = kAttnMaxKvHeads * 4;
-
-// q heads per kv head the attention kernel is built for.
-bool attention_group_supported(int group);
 
 // Rows per chunk when `rows` rows are attended: 128, 256, 384 or 512.
 int attention_chunk_rows(int rows);
@@ -147,12 +132,7 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
                                  float* logits, int logits_bf16, long long* out_idx,
                                  ArgmaxPartial* partials, const void* norm_w, float eps, hipStream_t stream);
 
-// lm_head argument checks of the C ABI (everything but the workspace),
-// clearing and then recording lsk_last_error's message; and the recorders
-// themselves, for entry points defined outside abi.cpp.
-int check_lm_head_call(const void* w_packed, int layout_id, int V, int K, const void* x, int M, int ldx,
-                       const float* logits_opt, int logits_mode, const long long* out_idx);
-int fail_call(int status, const char* message);
+// Records a HIP failure for lsk_last_error (defined in abi.cpp).
 int fail_hip_call(hipError_t err, const char* what);
 
 // Workspace bytes the split-K prefill path needs on `device` for this shape

@@ -16,7 +16,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <cstdio>
 #include <mutex>
 #include <vector>
 
@@ -44,7 +43,7 @@ int scratch_address(int device, void** out) {
     void* ptr = nullptr;
     hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (err != hipSuccess) return lsk::fail_hip_call(err, "hipGetSymbolAddress(static lm_head scratch)");
-    if (ptr == nullptr) return lsk::fail_call(LSK_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch");
+    if (ptr == nullptr) return lsk::fail(LSK_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch");
     g_scratch_ptr[device] = ptr;
   }
   *out = g_scratch_ptr[device];
@@ -60,12 +59,10 @@ extern "C" int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_
     return st;
   const size_t need = (size_t)M * (size_t)lsk::lm_head_partials(V) * sizeof(lsk::ArgmaxPartial);
   if (need > kScratchBytes) {
-    char msg[256];
-    snprintf(msg, sizeof(msg),
-             "M=%d rows over V=%d need %zu bytes of argmax partials; the static scratch holds %zu "
-             "(M * V / 32 * 8 bytes at most): use lsk_lm_head_argmax_bf16 with a workspace",
-             M, V, need, kScratchBytes);
-    return lsk::fail_call(LSK_ERR_INVALID, msg);
+    return lsk::fail(LSK_ERR_INVALID,
+                     "M=%d rows over V=%d need %zu bytes of argmax partials; the static scratch holds %zu "
+                     "(M * V / 32 * 8 bytes at most): use lsk_lm_head_argmax_bf16 with a workspace",
+                     M, V, need, kScratchBytes);
   }
   int device = 0;
   hipError_t err = hipGetDevice(&device);

@@ -249,6 +249,7 @@ class ResidentArena:
         skew = (-raw.data_ptr()) % 256  # device allocations are aligned already; host ones may not be
         self.buffer = raw[skew : skew + plan.arena_bytes]
         self._index = {e.name: e for e in plan.entries}
+        self.load_stats: dict[str, int] | None = None  # set by the pack loader
 
     def weight_names(self) -> set[str]:
         """Entries a pack must fill: everything but scratch and the KV cache."""
@@ -301,19 +302,119 @@ def _check_entry_layout(entry: ArenaEntry, layout_name: str, logical_shape) -> N
         raise ValueError(f"{entry.name}: the pack's shape {list(logical_shape)} != planned {list(entry.shape)}")
 
 
+# Bytes per read + host-to-device copy when a file region is staged.
+LOAD_CHUNK_BYTES = 256 << 20
+
+
+class _RegionReader:
+    """Reads byte ranges of pack files into arena ranges: straight into the
+    buffer for a host arena, through two pinned staging buffers (read one
+    while the other is copied) for a device arena."""
+
+    def __init__(self, arena: "ResidentArena", largest: int) -> None:
+        self.dst = arena.buffer
+        self.device = self.dst.device.type == "cuda"
+        self.stage, self.done = [], [None, None]
+        if self.device:
+            size = min(LOAD_CHUNK_BYTES, max(largest, 1))
+            self.stage = [torch.empty(size, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        self.reads = 0
+        self.copies = 0
+
+    def read(self, path: Path, file_offset: int, nbytes: int, arena_offset: int) -> None:
+        with open(path, "rb", buffering=0) as f:
+            f.seek(file_offset)
+            if not self.device:
+                got = f.readinto(memoryview(self.dst[arena_offset : arena_offset + nbytes].numpy()))
+                if got != nbytes:
+                    raise ValueError(f"{path}: {got} of {nbytes} bytes at offset {file_offset} (truncated file)")
+                self.reads += 1
+                self.copies += 1
+                return
+            done, i = 0, 0
+            while done < nbytes:
+                n = min(len(self.stage[0]), nbytes - done)
+                slot = i % 2
+                if self.done[slot] is not None:
+                    self.done[slot].synchronize()
+                got = f.readinto(memoryview(self.stage[slot].numpy())[:n])
+                if got != n:
+                    raise ValueError(f"{path}: {done + got} of {nbytes} bytes at offset {file_offset} (truncated file)")
+                self.dst[arena_offset + done : arena_offset + done + n].copy_(self.stage[slot][:n], non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record()
+                self.done[slot] = ev
+                done += n
+                i += 1
+                self.copies += 1
+            self.reads += 1
+
+    def finish(self) -> None:
+        for ev in self.done:
+            if ev is not None:
+                ev.synchronize()
+
+
+def load_pack_into_arena(root: Path, manifest, arena: "ResidentArena") -> dict[str, int]:
+    """Fill every planned weight of `arena` from the pack at `root` by
+    direct file offsets.  A file whose tensors sit at the same relative
+    offsets as their arena entries (the layout the packer writes) is one
+    read and one copy of its whole data region; any other file is one read
+    of its region with a copy per tensor.  Refuses a pack that misses a
+    planned weight or stores one in another layout or size.  Returns load
+    statistics: files, bulk (files loaded as one image), per_tensor (tensors
+    copied one by one), bytes."""
+    plan = arena.plan
+    planned = arena.weight_names()
+    by_file: dict[str, list] = {}
+    for t in manifest.tensors:
+        if t.name in planned:
+            e = plan.entry(t.name)
+            _check_entry_layout(e, t.layout, t.logical_shape)
+            if t.size_bytes != e.nbytes:
+                raise ValueError(f"{t.name}: the pack stores {t.size_bytes} bytes, the plan needs {e.nbytes}")
+            by_file.setdefault(t.file, []).append(t)
+    missing = sorted(planned - {t.name for ts in by_file.values() for t in ts})
+    if missing:
+        raise ValueError(f"{root}: the pack has no tensor for {len(missing)} planned weights, e.g. {missing[:3]}")
+    largest = max(ts[-1].file_offset_bytes + ts[-1].size_bytes - ts[0].file_offset_bytes
+                  for ts in (sorted(v, key=lambda t: t.file_offset_bytes) for v in by_file.values()))
+    reader = _RegionReader(arena, largest)
+    stats = {"files": 0, "bulk": 0, "per_tensor": 0, "bytes": 0}
+    for file_name, ts in by_file.items():
+        ts = sorted(ts, key=lambda t: t.file_offset_bytes)
+        f0, a0 = ts[0].file_offset_bytes, plan.entry(ts[0].name).offset
+        span = ts[-1].file_offset_bytes + ts[-1].size_bytes - f0
+        inside = {e.name for e in plan.entries if e.offset < a0 + span and e.end > a0}
+        image = inside == {t.name for t in ts} and all(
+            t.file_offset_bytes - f0 == plan.entry(t.name).offset - a0 for t in ts)
+        if image:
+            reader.read(root / file_name, f0, span, a0)
+            stats["bulk"] += 1
+        else:
+            for t in ts:
+                reader.read(root / file_name, t.file_offset_bytes, t.size_bytes, plan.entry(t.name).offset)
+            stats["per_tensor"] += len(ts)
+        stats["files"] += 1
+        stats["bytes"] += sum(t.size_bytes for t in ts)
+    reader.finish()
+    return stats
+
+
 def materialize_qwen_semantic_stack_from_leanpack(
     pack_dir: str | Path,
     *,
     device: str | torch.device = "cuda:0",
     include_output_head: bool = True,
     max_rows: int = 16,
-    buckets: Iterable[BucketSpec] = DEFAULT_BUCKETS,
+    buckets: Iterable[BucketSpec] | None = None,
 ):
     """Load a leanpack/v1 artifact into one resident arena and build the
     runtime (replaces src/leanstack/leanserve.py:470-530, which copies each
-    tensor to its own allocation).  Returns (runtime, arena)."""
-    from safetensors import safe_open
-
+    tensor to its own allocation).  The KV cache is sized for the manifest's
+    buckets (as the reference's planner reads them, leanserve.py:199-202,
+    :331-377) unless `buckets` is given.  Returns (runtime, arena); the
+    arena's `load_stats` records how the files were read."""
     from .pack import geometry_from_manifest, load_packed_artifact_manifest
     from .runtime import (
         QwenSemanticAttentionRuntime,
@@ -327,24 +428,11 @@ def materialize_qwen_semantic_stack_from_leanpack(
     root = Path(pack_dir)
     manifest = load_packed_artifact_manifest(root)
     g = geometry_from_manifest(manifest)
+    if buckets is None:
+        buckets = [BucketSpec(b.key, b.prompt_tokens, b.max_new_tokens) for b in manifest.buckets]
     plan = build_resident_buffer_plan(g, buckets=buckets, max_rows=max_rows, include_lm_head=include_output_head)
     arena = ResidentArena(plan, device)
-    by_file: dict[str, list] = {}
-    for t in manifest.tensors:
-        if t.name in arena.weight_names():
-            _check_entry_layout(plan.entry(t.name), t.layout, t.logical_shape)
-            by_file.setdefault(t.file, []).append(t)
-    missing = sorted(arena.weight_names() - {t.name for ts in by_file.values() for t in ts})
-    if missing:
-        raise ValueError(f"{root}: the pack has no tensor for {len(missing)} planned weights, e.g. {missing[:3]}")
-    for file_name, entries in by_file.items():
-        with safe_open(str(root / file_name), framework="pt", device="cpu") as handle:
-            for t in entries:
-                value = handle.get_tensor(t.name)
-                if t.layout == "rowmajor":
-                    arena.view(t.name).copy_(value.view(arena.plan.entry(t.name).shape))
-                else:
-                    arena.store_packed(t.name, value)
+    arena.load_stats = load_pack_into_arena(root, manifest, arena)
 
     cfg = QwenServeConfig(
         vocab_size=g.vocab_size, hidden_size=g.hidden_size, intermediate_size=g.intermediate_size,

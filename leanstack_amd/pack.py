@@ -5,25 +5,36 @@ writes row-major fused tensors per layer -- qkv_proj = cat(q, k, v) and
 gate_up_proj = cat(gate, up) (:269-286) -- plus a separate lm_head copy
 (:318-323) and a manifest.  leanpack/v1 keeps the same file split and
 manifest fields (so the reference's manifest readers still find geometry,
-files and tensors) and changes the projection tensors: each is stored as the
-flat 1-D bf16 tensor of its packed layout (include/leanstack_amd.h), with the
-logical [N, K] shape and layout name recorded per tensor.  The lm_head copy
-is stored packed too: the row-major embedding serves the token gather and the
-packed copy serves the greedy head, so the reference's duplicate becomes a
-useful one.  A manifest `layout` section names the tile geometry and the
-target GPU; loaders refuse an unknown format or layout.
+buckets, files and tensors) and changes three things:
+
+  - Projection tensors are stored as the flat 1-D bf16 tensor of their packed
+    layout (include/leanstack_amd.h), with the logical [N, K] shape and the
+    layout name recorded per tensor.  The lm_head copy is stored packed too:
+    the row-major embedding serves the token gather, the packed copy the
+    greedy head, so the reference's duplicate becomes a useful one.
+  - Direct offset loading (the format doc's missing "mmap-style offset
+    loading", docs/LEANPACK_FORMAT.md:73-78): every file is still a valid
+    safetensors file, but each tensor's data starts at a 4096-byte aligned
+    file offset, recorded in the manifest (`file_offset_bytes`), and the
+    tensors of a file follow the resident arena's order and alignment, so a
+    file's data region is a byte image of a contiguous arena range.  The
+    loader reads it once and copies it to the device once, straight into the
+    arena; gaps are filled by zero `__pad__` tensors, which keeps the
+    safetensors byte buffer free of holes.
+  - A manifest `layout` section names the tile geometry and the target GPU;
+    loaders refuse an unknown format or layout.
 """
 
 from __future__ import annotations
 
 import json
+import struct
 from dataclasses import asdict, dataclass, field
 from datetime import datetime, timezone
 from pathlib import Path
 from typing import Any, Mapping
 
 import torch
-from safetensors.torch import save_file
 
 from . import _lib
 from .geometry import QWEN3_4B, QwenGeometry
@@ -43,6 +54,12 @@ LAYOUT_SECTION = {
 }
 
 
+# Alignment of every tensor's data in a pack file: the resident arena's entry
+# alignment (leanserve.ARENA_ALIGNMENT), so that a file's data region and its
+# arena range have the same layout.
+FILE_ALIGNMENT = 4096
+
+
 @dataclass(frozen=True)
 class PackedTensorEntry:
     name: str
@@ -53,9 +70,10 @@ class PackedTensorEntry:
     logical_shape: list[int]    # [N, K] of the weight as the model uses it
     layout: str                 # "rowmajor" or a packed layout name
     numel: int
-    logical_offset_bytes: int
+    logical_offset_bytes: int   # offset inside the file's data region (aligned)
     size_bytes: int
     source_tensors: list[str]
+    file_offset_bytes: int = 0  # absolute byte offset of the data in the file (FILE_ALIGNMENT aligned)
 
 
 @dataclass(frozen=True)
@@ -63,6 +81,69 @@ class PackedFileEntry:
     file: str
     tensor_count: int
     size_bytes: int
+    data_offset_bytes: int = 0  # where the (aligned) data region starts in the file
+    data_bytes: int = 0         # length of the data region, padding included
+
+
+# Manifest metadata of the reference's leanpack (src/leanstack/pack.py:64-100).
+@dataclass(frozen=True)
+class BucketEntry:
+    key: str
+    prompt_tokens: int
+    max_new_tokens: int
+
+
+@dataclass(frozen=True)
+class SpeculativeModeEntry:
+    key: str
+    draft_layer_count: int
+    proposal_len: int
+
+
+@dataclass(frozen=True)
+class DraftHeadEntry:
+    key: str
+    draft_layer_count: int
+    file: str
+    tensor_name: str
+    input_size: int
+    output_size: int
+    fit_samples: int
+    ridge_lambda: float
+
+
+# The Qwen3-4B contract's exact prompt buckets and the benchmark buckets built
+# on them (src/leanstack/model_registry.py:37, src/leanstack/benchmark.py:
+# 59-93), and the speculative modes the reference records (pack.py:178-193:
+# a 12-layer draft proposing 4 or 2 tokens).
+QWEN_EXACT_PROMPT_BUCKETS = (64, 512, 1024)
+QWEN_BUCKETS = (
+    BucketEntry("decode_64_256", 64, 256),
+    BucketEntry("decode_64_512", 64, 512),
+    BucketEntry("prefill_1024_64", 1024, 64),
+)
+
+# The kernels a runtime on this pack needs: the C-ABI entry points of
+# libleanstack_amd.so that the dispatch calls.
+REQUIRED_KERNELS = (
+    "lsk_linear_bf16",
+    "lsk_rmsnorm_linear_bf16",
+    "lsk_decode_attention_at_bf16",
+    "lsk_lm_head_argmax_bf16",
+    "lsk_rmsnorm_lm_head_argmax_bf16",
+)
+BACKEND_POLICY = (
+    "Every projection, the decode attention step and the greedy head run on hand-written HIP kernels for gfx950 "
+    "behind the C ABI of libleanstack_amd.so.",
+    "No torch.compile, Triton or library GEMM on the hot path; a missing library or a rejected argument raises "
+    "instead of falling back.",
+    "Weights stay resident in one device arena in the packed mfma16x32 layouts recorded per tensor.",
+)
+
+
+def speculative_modes(num_hidden_layers: int) -> list[SpeculativeModeEntry]:
+    draft = min(12, max(num_hidden_layers - 1, 1))
+    return [SpeculativeModeEntry("draft12_k4", draft, 4), SpeculativeModeEntry("draft12_k2", draft, 2)]
 
 
 @dataclass(frozen=True)
@@ -77,6 +158,12 @@ class PackedArtifactManifest:
     geometry: dict[str, int]
     model_hparams: dict[str, Any]
     layout: dict[str, Any]
+    exact_prompt_buckets: list[int] = field(default_factory=list)
+    buckets: list[BucketEntry] = field(default_factory=list)
+    speculative_modes: list[SpeculativeModeEntry] = field(default_factory=list)
+    draft_heads: list[DraftHeadEntry] = field(default_factory=list)
+    required_kernels: list[str] = field(default_factory=list)
+    backend_policy: list[str] = field(default_factory=list)
     files: list[PackedFileEntry] = field(default_factory=list)
     tensors: list[PackedTensorEntry] = field(default_factory=list)
 
@@ -97,6 +184,12 @@ class PackedArtifactManifest:
             geometry=dict(payload.get("geometry", {})),
             model_hparams=dict(payload.get("model_hparams", {})),
             layout=dict(payload.get("layout", {})),
+            exact_prompt_buckets=[int(b) for b in payload.get("exact_prompt_buckets", [])],
+            buckets=[BucketEntry(**b) for b in payload.get("buckets", [])],
+            speculative_modes=[SpeculativeModeEntry(**m) for m in payload.get("speculative_modes", [])],
+            draft_heads=[DraftHeadEntry(**h) for h in payload.get("draft_heads", [])],
+            required_kernels=list(payload.get("required_kernels", [])),
+            backend_policy=list(payload.get("backend_policy", [])),
             files=[PackedFileEntry(**f) for f in payload.get("files", [])],
             tensors=[PackedTensorEntry(**t) for t in payload.get("tensors", [])],
         )
@@ -188,25 +281,72 @@ def synthetic_qwen_checkpoint(geometry: QwenGeometry = QWEN3_4B, *, seed: int = 
     return out
 
 
-def _entries(file_name: str, tensors: dict[str, torch.Tensor], meta: dict[str, tuple]) -> tuple[list, int]:
-    entries, offset = [], 0
+_ST_DTYPES = {torch.bfloat16: "BF16", torch.float32: "F32", torch.uint8: "U8"}
+
+
+def _align(n: int) -> int:
+    return -(-n // FILE_ALIGNMENT) * FILE_ALIGNMENT
+
+
+def write_aligned_safetensors(path: Path, tensors: dict[str, torch.Tensor]) -> tuple[int, int, dict[str, int]]:
+    """Write `tensors` (in this order) as a safetensors file whose data
+    region starts at a FILE_ALIGNMENT boundary and in which every tensor's
+    data starts at a FILE_ALIGNMENT offset from it, the gaps filled by zero
+    `__pad__.<i>` uint8 tensors (the format requires a byte buffer without
+    holes).  The header is padded with spaces, which the format allows.
+    Returns (data_offset, data_bytes, {name: offset inside the data region})."""
+    header: dict[str, Any] = {"__metadata__": {"format": "pt", "layout": FORMAT_VERSION}}
+    offsets: dict[str, int] = {}
+    pads: list[tuple[int, int]] = []
+    pos = 0
+    for i, (name, t) in enumerate(tensors.items()):
+        if t.dtype not in _ST_DTYPES:
+            raise ValueError(f"{name}: dtype {t.dtype} is not stored by leanpack")
+        start = _align(pos)
+        if start > pos:
+            header[f"__pad__.{i}"] = {"dtype": "U8", "shape": [start - pos], "data_offsets": [pos, start]}
+            pads.append((pos, start))
+        size = t.numel() * t.element_size()
+        header[name] = {"dtype": _ST_DTYPES[t.dtype], "shape": list(t.shape), "data_offsets": [start, start + size]}
+        offsets[name] = start
+        pos = start + size
+    raw = json.dumps(header, separators=(",", ":")).encode("utf-8")
+    data_offset = _align(8 + len(raw))
+    raw += b" " * (data_offset - 8 - len(raw))
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(raw)))
+        f.write(raw)
+        end = 0
+        for name, t in tensors.items():
+            start = offsets[name]
+            if start > end:
+                f.write(bytes(start - end))
+            f.write(t.detach().contiguous().cpu().view(torch.uint8).numpy().tobytes())
+            end = start + t.numel() * t.element_size()
+    return data_offset, pos, offsets
+
+
+def _entries(file_name: str, tensors: dict[str, torch.Tensor], meta: dict[str, tuple], data_offset: int,
+             offsets: dict[str, int]) -> list[PackedTensorEntry]:
+    entries = []
     for name, t in tensors.items():
         role, logical, layout, sources = meta[name]
-        size = t.numel() * t.element_size()
         entries.append(PackedTensorEntry(
             name=name, role=role, file=file_name, dtype=str(t.dtype).removeprefix("torch."), shape=list(t.shape),
-            logical_shape=list(logical), layout=layout, numel=t.numel(), logical_offset_bytes=offset,
-            size_bytes=size, source_tensors=list(sources)))
-        offset += size
-    return entries, offset
+            logical_shape=list(logical), layout=layout, numel=t.numel(), logical_offset_bytes=offsets[name],
+            size_bytes=t.numel() * t.element_size(), source_tensors=list(sources),
+            file_offset_bytes=data_offset + offsets[name]))
+    return entries
 
 
 def build_qwen_leanpack(tensors: Mapping[str, torch.Tensor], output_dir: str | Path, *,
                         geometry: QwenGeometry = QWEN3_4B, model_key: str = "qwen",
                         semantic_model_id: str | None = "Qwen/Qwen3-4B-Base", source_model_path: str = "",
-                        overwrite: bool = False) -> PackedArtifactManifest:
+                        overwrite: bool = False, exact_prompt_buckets=QWEN_EXACT_PROMPT_BUCKETS,
+                        buckets=QWEN_BUCKETS) -> PackedArtifactManifest:
     """Pack a Qwen3 checkpoint (Hugging Face tensor names, row-major) into
-    leanpack/v1 at output_dir."""
+    leanpack/v1 at output_dir.  `buckets` are recorded in the manifest and
+    size the loader's KV cache (BucketEntry list)."""
     g = geometry
     root = Path(output_dir)
     if root.exists() and any(root.iterdir()) and not overwrite:
@@ -218,10 +358,10 @@ def build_qwen_leanpack(tensors: Mapping[str, torch.Tensor], output_dir: str | P
 
     def write(file_name: str, group: dict[str, torch.Tensor], meta: dict[str, tuple]) -> None:
         group = {k: v.contiguous() for k, v in group.items()}
-        save_file(group, str(root / file_name))
-        es, _ = _entries(file_name, group, meta)
-        files.append(PackedFileEntry(file_name, len(group), (root / file_name).stat().st_size))
-        entries.extend(es)
+        data_offset, data_bytes, offsets = write_aligned_safetensors(root / file_name, group)
+        files.append(PackedFileEntry(file_name, len(group), (root / file_name).stat().st_size, data_offset,
+                                     data_bytes))
+        entries.extend(_entries(file_name, group, meta, data_offset, offsets))
 
     embed = tensors["model.embed_tokens.weight"].to(torch.bfloat16)
     write("embeddings.safetensors", {"model.embed_tokens.weight": embed},
@@ -283,6 +423,12 @@ def build_qwen_leanpack(tensors: Mapping[str, torch.Tensor], output_dir: str | P
         },
         model_hparams={"rms_norm_eps": g.rms_norm_eps, "rope_theta": g.rope_theta},
         layout=dict(LAYOUT_SECTION),
+        exact_prompt_buckets=list(exact_prompt_buckets),
+        buckets=list(buckets),
+        speculative_modes=speculative_modes(g.num_hidden_layers),
+        draft_heads=[],
+        required_kernels=list(REQUIRED_KERNELS),
+        backend_policy=list(BACKEND_POLICY),
         files=files,
         tensors=entries,
     )

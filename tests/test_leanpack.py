@@ -87,6 +87,84 @@ def test_materialize_round_trips_every_tensor(tiny_pack):
     assert runtime.config.num_key_value_heads == 2 and runtime.layers[0].attention.num_key_value_groups == 2
 
 
+def test_files_are_aligned_safetensors(tiny_pack):
+    """Every file opens with safetensors and holds the packed tensors; each
+    tensor's data starts at a 4096-byte file offset that the manifest
+    records, and reading those bytes at that offset gives the tensor."""
+    from safetensors import safe_open
+
+    from leanstack_amd.layout import pack_tensor
+
+    ckpt, out, manifest = tiny_pack
+    expect = {"model.embed_tokens.weight": ckpt["model.embed_tokens.weight"],
+              "layers.1.attention.o_proj.weight": pack_tensor(ckpt[hf_layer_names(1)["o_proj"]], _lib.LAYOUT_MFMA16X32),
+              "layers.0.input_layernorm.weight": ckpt[hf_layer_names(0)["input_layernorm"]]}
+    for t in manifest.tensors:
+        assert t.file_offset_bytes % 4096 == 0 and t.logical_offset_bytes % 4096 == 0
+        with safe_open(str(out / t.file), framework="pt") as f:
+            stored = f.get_tensor(t.name)
+        assert list(stored.shape) == t.shape and stored.numel() * 2 == t.size_bytes
+        raw = (out / t.file).read_bytes()[t.file_offset_bytes : t.file_offset_bytes + t.size_bytes]
+        assert raw == stored.contiguous().view(torch.uint8).numpy().tobytes()
+        if t.name in expect:
+            assert torch.equal(stored.view(torch.int16), expect[t.name].reshape(stored.shape).view(torch.int16))
+    for fe in manifest.files:
+        assert fe.data_offset_bytes % 4096 == 0 and fe.size_bytes == (out / fe.file).stat().st_size
+
+
+def test_manifest_carries_the_reference_metadata(tiny_pack):
+    """Buckets, speculative modes, required kernels and backend policy, the
+    leanpack/v0 fields the reference's loader and planner read
+    (src/leanstack/pack.py:95-100, leanserve.py:199-202)."""
+    _, out, manifest = tiny_pack
+    assert manifest.exact_prompt_buckets == [64, 512, 1024]
+    assert [(b.key, b.prompt_tokens, b.max_new_tokens) for b in manifest.buckets] == [
+        ("decode_64_256", 64, 256), ("decode_64_512", 64, 512), ("prefill_1024_64", 1024, 64)]
+    assert [m.key for m in manifest.speculative_modes] == ["draft12_k4", "draft12_k2"]
+    assert manifest.speculative_modes[0].draft_layer_count == 1  # 2-layer model: min(12, L - 1)
+    assert "lsk_linear_bf16" in manifest.required_kernels and manifest.backend_policy
+    assert load_packed_artifact_manifest(out).buckets == manifest.buckets
+
+
+def test_loader_reads_each_file_as_one_arena_image(tiny_pack):
+    """Every file's data region is a byte image of its arena range: one read
+    and one copy per file, no per-tensor reads; the KV cache is sized from
+    the manifest's buckets (1088 tokens -> 1088 rows in pages of 16)."""
+    _, out, manifest = tiny_pack
+    runtime, arena = materialize_qwen_semantic_stack_from_leanpack(out, device="cpu")
+    assert arena.load_stats == {"files": len(manifest.files), "bulk": len(manifest.files), "per_tensor": 0,
+                                "bytes": sum(t.size_bytes for t in manifest.tensors)}
+    kv = arena.plan.entry("kv_cache")
+    assert kv.shape[4] == 1088 and [b.key for b in arena.plan.buckets] == [b.key for b in manifest.buckets]
+
+
+def test_loader_places_tensors_one_by_one_when_offsets_differ(tiny_pack):
+    """With an arena of another alignment the files are no longer images of
+    arena ranges: the loader copies each tensor to its entry, same result."""
+    from leanstack_amd.leanserve import ResidentArena, build_resident_buffer_plan, load_pack_into_arena
+    from leanstack_amd.pack import geometry_from_manifest
+
+    ckpt, out, manifest = tiny_pack
+    plan = build_resident_buffer_plan(geometry_from_manifest(manifest), buckets=(), alignment=8192)
+    arena = ResidentArena(plan, "cpu")
+    stats = load_pack_into_arena(out, manifest, arena)
+    assert stats["bulk"] < stats["files"] and stats["per_tensor"] > 0
+    assert torch.equal(arena.view("model.embed_tokens.weight"), ckpt["model.embed_tokens.weight"])
+    assert torch.equal(arena.packed("layers.1.mlp.down_proj.weight").unpack(), ckpt[hf_layer_names(1)["down_proj"]])
+
+
+def test_loader_refuses_a_truncated_file(tiny_pack, tmp_path):
+    import shutil
+
+    _, out, _ = tiny_pack
+    bad = tmp_path / "short"
+    shutil.copytree(out, bad)
+    data = (bad / "layer-001.safetensors").read_bytes()
+    (bad / "layer-001.safetensors").write_bytes(data[: len(data) - 4096])
+    with pytest.raises(ValueError, match="truncated"):
+        materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
+
+
 def _copy_pack(src, dst, edit):
     """A copy of the pack at dst whose manifest payload went through edit()."""
     import shutil
