@@ -71,6 +71,15 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def profiled_mfma_util() -> dict | None:
+    """MfmaUtil per prefill projection at M = 2048 as the committed counter
+    profile measured it (profiles/prefill_counters.json), or None."""
+    path = REPO / "profiles" / "prefill_counters.json"
+    if not path.exists():
+        return None
+    return json.loads(path.read_text()).get("mfma_util_pct_m2048")
+
+
 def measured_traffic(kernel_label: str):
     """HBM bytes per launch of the roofline kernel, as the committed counter
     profile measured it (profiles/hbm_traffic.json), or None."""
@@ -85,10 +94,24 @@ def measured_traffic(kernel_label: str):
     return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's description."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+CPU_LAYERS = 4  # 808 MB of distinct weights: larger than any host L3, so the sample streams DRAM
+
+
 def cpu_baseline(g, seconds: float) -> dict:
     """The reference's CPU torch path (torch.mv in bf16 + F.silu*mul, via the
-    oracle) on this host's cores, over a bounded sample: two distinct random
-    Qwen3-4B layers, M = 1, repeated for about `seconds`."""
+    oracle) on this host's cores, over a bounded sample: CPU_LAYERS distinct
+    random Qwen3-4B layers cycled in order, M = 1, for about `seconds`."""
     import torch
 
     from oracle import projections as ref
@@ -96,7 +119,7 @@ def cpu_baseline(g, seconds: float) -> dict:
     threads = torch.get_num_threads()
     gen = torch.Generator(device="cpu").manual_seed(0)
     layers = []
-    for _ in range(2):
+    for _ in range(CPU_LAYERS):
         layers.append({
             name: (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16)
             for name, (n, k) in g.projections().items()
@@ -113,7 +136,7 @@ def cpu_baseline(g, seconds: float) -> dict:
     done = 0
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        one_layer(layers[done % 2])
+        one_layer(layers[done % CPU_LAYERS])
         done += 1
     elapsed = time.perf_counter() - t0
     gbs = done * g.layer_bytes(1) / elapsed / 1e9
@@ -123,9 +146,9 @@ def cpu_baseline(g, seconds: float) -> dict:
         "cores": threads,
         "kind": "port",
         "sample": (f"{done} Qwen3-4B decode layers at M=1 (torch.mv bf16 qkv/o/gate_up/down + F.silu*mul, "
-                   f"2 distinct random layers alternated) in {elapsed:.1f} s; "
-                   f"{elapsed / done * 1e6:.0f} us/layer; cpu={platform.processor() or platform.machine()}, "
-                   f"os.cpu_count={os.cpu_count()}"),
+                   f"{CPU_LAYERS} distinct random layers = {CPU_LAYERS * g.layer_bytes(1) / 1e6:.0f} MB cycled) in "
+                   f"{elapsed:.1f} s; {elapsed / done * 1e6:.0f} us/layer; cpu={cpu_model()}, "
+                   f"os.cpu_count={os.cpu_count()}, torch threads={threads}"),
     }
 
 
@@ -357,6 +380,26 @@ def main() -> int:
             prefill[m] = row
             log(f"prefill M={m}: layer {row['layer_us']} us, {row['layer_TFLOP/s']} TFLOP/s")
 
+    # Prefill roofline at 2048 tokens: the layer's four GEMMs against dense
+    # BF16 MFMA peak (2.5 PFLOP/s), TFLOP/s = 2 M N K / time.
+    prefill_roofline = None
+    if 2048 in prefill:
+        row = prefill[2048]
+        achieved_tf = row["layer_TFLOP/s"]
+        prefill_roofline = {
+            "bound": "mfma",
+            "kernel": "gemm_wdx_kernel (qkv, o, gate_up + silu*up, down at 2048 tokens)",
+            "flops_per_layer": G.layer_flops(2048),
+            "achieved": achieved_tf,
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved_tf / BF16_PEAK_TFLOPS, 4),
+            "layer_us": row["layer_us"],
+            "per_projection_TFLOP/s": {n: row[n]["TFLOP/s"] for n in G.projections()},
+            "mfma_util_pct": profiled_mfma_util(),
+            "mfma_util_source": "profiles/prefill_gemm_counters.md (rocprofv3 --pmc MfmaUtil, bench.py --pmc-prefill)",
+        }
+
     cpu = None
     if not args.quick:
         cpu = cpu_baseline(G, args.cpu_seconds)
@@ -395,6 +438,7 @@ def main() -> int:
             "traffic_source": "profiles/decode_projections_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                               "scaled by a 1 GiB copy in the same run)",
         },
+        "roofline_prefill": prefill_roofline,
         "cpu_baseline": cpu,
         "detail": {
             "stack_frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),

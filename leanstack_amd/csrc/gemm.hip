@@ -23,6 +23,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "lsk_internal.h"
@@ -471,7 +472,8 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 
 }  // namespace big
 
-// Weights-direct variant of the 256x256x64 kernel.  Each wave loads its own
+// Weights-direct variant of the 256x256x64 kernel (and of a 192x256x64 one:
+// A = 3 32-row weight tiles per wave instead of 4, chosen by choose_tiles).  Each wave loads its own
 // weight fragments from global memory straight into registers: a packed 1 KB
 // tile already is MFMA operand data in lane order, so a 32-row A fragment is
 // two 512-byte contiguous runs and needs no LDS staging.  Only the
@@ -484,6 +486,10 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 namespace wdx {
 
 constexpr int BN = 256, BM = 256, BK = 64;
+// Weight rows per block with A 32-row tiles per wave (two waves across N):
+// A = 4 -> 256 rows, A = 3 -> 192 rows (QKV: 32 weight blocks instead of 24).
+template <int A>
+constexpr int kBN = 64 * A;
 constexpr int kThreads = 256;
 constexpr int kXStageBytes = BM * BK * 2;  // 32 KB of activation fragments per stage
 constexpr int kXChunks = 8;                // 16-byte activation chunks per thread per stage
@@ -503,17 +509,19 @@ struct XRegs {
   bf16x8_t v[kXChunks];
 };
 
+template <int A>
 struct WFrags {
-  bf16x8_t v[4][4];  // [16-K step q][32-row tile a]
+  bf16x8_t v[4][A];  // [16-K step q][32-row tile a]
 };
 
 // A fragment (32 rows x 16 K) of tile a, step q: lane (li, kg) takes row li of
 // the two 16-row packed tiles 2a, 2a+1 and K chunk 2(q&1)+kg of k-tile q/2.
-__device__ __forceinline__ void load_w(WFrags& f, const bf16x8_t* __restrict__ wl, int KT, int s) {
+template <int A>
+__device__ __forceinline__ void load_w(WFrags<A>& f, const bf16x8_t* __restrict__ wl, int KT, int s) {
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int a = 0; a < 4; ++a) f.v[q][a] = wl[((size_t)(2 * a) * KT + 2 * s + (q >> 1)) * 64 + (q & 1) * 32];
+    for (int a = 0; a < A; ++a) f.v[q][a] = wl[((size_t)(2 * a) * KT + 2 * s + (q >> 1)) * 64 + (q & 1) * 32];
 }
 
 __device__ __forceinline__ void load_x(XRegs& r, const __bf16* __restrict__ x, int ldx, int M, int m0, int s,
@@ -553,7 +561,8 @@ struct Args {
 // 16-K step publishes buffer (s+1)&1 and retires every read of buffer s&1.
 // Stage indices past s1 are clamped: those loads stay in bounds and the data
 // they stage is never multiplied.
-__device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, unsigned char* lds, int nb, int mb,
+template <int A>
+__device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, unsigned char* lds, int nb, int mb,
                                          int s0, int s1) {
   // Opaque per call: keeps the per-lane offsets below from being hoisted out
   // of a caller's loop over blocks, where they would stay live (and spill)
@@ -570,7 +579,8 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
   const int KT = g.KT;
 
   // This lane's element of weight fragment (a=0, q=0) at stage 0.
-  const bf16x8_t* wl = g.w + ((size_t)(nb * (BN / kTileRows) + wn * 8 + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
+  const bf16x8_t* wl =
+      g.w + ((size_t)(nb * (kBN<A> / kTileRows) + wn * 2 * A + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
   int x_lane[4];
 #pragma unroll
   for (int q = 0; q < 4; ++q) x_lane[q] = wm * 4 * 4096 + q * 1024 + (((li ^ (4 * q + 2 * kg)) + 32 * kg) << 4);
@@ -581,16 +591,19 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
   };
   auto mfma_step = [&](const bf16x8_t* fa, const bf16x8_t* fb) {
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < A; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(fa[a], fb[b], acc[a][b]);
   };
 
   XRegs xr;
-  WFrags wf0, wf1;
+  WFrags<A> wf0, wf1;
   bf16x8_t fb0[4], fb1[4];
 
-  auto stage = [&](int s, const WFrags& wc, WFrags& wn_) {
+  // Interleave groups per 16-K step: 4A MFMAs with the step's LDS and
+  // global traffic.
+  constexpr int kM = 4 * A;
+  auto stage = [&](int s, const WFrags<A>& wc, WFrags<A>& wn_) {
     const unsigned char* cur = lds + (s & 1) * kXStageBytes;
     unsigned char* nxt = lds + ((s + 1) & 1) * kXStageBytes;
     const int sw = min(s + 1, s1 - 1);
@@ -607,7 +620,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
       __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
+    for (int i = 0; i < kM - 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
     }
@@ -626,7 +639,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+    if constexpr (kM > 12) __builtin_amdgcn_sched_group_barrier(kSchedMfma, kM - 12, 0);
 
     __builtin_amdgcn_sched_barrier(0);
     read_b(fb1, cur, 3);
@@ -643,7 +656,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kM - 8, 0);
 
     __syncthreads();
     read_b(fb0, nxt, 0);
@@ -653,7 +666,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 12, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kM - 4, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -675,7 +688,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[4][4], const Args& g, u
 // Epilogue of this lane's 32x32 tile (a, b) of block (nb, mb).  src(p)
 // returns elements 2p, 2p+1 of the lane's 16 fp32 results of the tile.
 // Lane l of tile (a, b) holds D[8*(j/4) + 4*(l/32) + j%4][l%32], j = 0..15.
-template <int EPI, typename Src>
+template <int EPI, int A, typename Src>
 __device__ __forceinline__ void store_one_tile(Src src, const Args& g, int nb, int mb, int a, int b) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -685,7 +698,7 @@ __device__ __forceinline__ void store_one_tile(Src src, const Args& g, int nb, i
   const int kg = lane >> 5;
   const int m = mb * BM + (wm * 4 + b) * 32 + li;
   if (m >= g.M) return;
-  const int an = nb * 8 + wn * 4 + a;  // global 32-row tile index
+  const int an = nb * 2 * A + wn * A + a;  // global 32-row tile index
   if constexpr (EPI == static_cast<int>(Epilogue::kSiluMul)) {
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) {
@@ -717,19 +730,20 @@ __device__ __forceinline__ void store_one_tile(Src src, const Args& g, int nb, i
 }
 
 // Epilogue of the whole block straight from the accumulators.
-template <int EPI>
-__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[4][4], const Args& g, int nb, int mb) {
+template <int EPI, int A>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[A][4], const Args& g, int nb, int mb) {
 #pragma unroll
   for (int b = 0; b < 4; ++b)
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
-      store_one_tile<EPI>([&](int p) { return make_float2(acc[a][b][2 * p], acc[a][b][2 * p + 1]); }, g, nb, mb, a,
+    for (int a = 0; a < A; ++a)
+      store_one_tile<EPI, A>([&](int p) { return make_float2(acc[a][b][2 * p], acc[a][b][2 * p + 1]); }, g, nb, mb, a,
                           b);
 }
 
-__device__ __forceinline__ void zero(f32x16_t (&acc)[4][4]) {
+template <int A>
+__device__ __forceinline__ void zero(f32x16_t (&acc)[A][4]) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < A; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
@@ -793,12 +807,12 @@ struct Split {
   unsigned spin_limit;      // polls of the arrival word before a wait gives up
 };
 
-template <int EPI>
+template <int EPI, int A>
 __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXStageBytes];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
-  f32x16_t acc[4][4];
+  f32x16_t acc[A][4];
   zero(acc);
 
   if (b < k.dp) {
@@ -808,7 +822,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
     int nb, mb;
     tile_coords(t, g.n_blocks, g.m_blocks, nb, mb);
     mainloop(acc, g, lds, nb, mb, 0, g.KT / 2);
-    store_tile<EPI>(acc, g, nb, mb);
+    store_tile<EPI, A>(acc, g, nb, mb);
     return;
   }
   // Chunk-major order: all split blocks' chunk 0, then chunk 1, ...
@@ -840,7 +854,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   {
     const unsigned slot = (unsigned)r * (unsigned)kSkPartialBytes;
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < A; ++a)
 #pragma unroll
       for (int bb = 0; bb < 4; ++bb)
 #pragma unroll
@@ -876,8 +890,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   // Sum this workgroup's share of the block's tiles over the S chunks.
   const unsigned first = (unsigned)i * (unsigned)kSkPartialBytes;
   const unsigned chunk_stride = (unsigned)k.R * (unsigned)kSkPartialBytes;
-  const int ab1 = (chunk + 1) * 16 / k.S;
-  for (int ab = chunk * 16 / k.S; ab < ab1; ++ab) {
+  const int ab1 = (chunk + 1) * 4 * A / k.S;
+  for (int ab = chunk * 4 * A / k.S; ab < ab1; ++ab) {
     f32x4_t sum[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -896,7 +910,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
       for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
                                                    __builtin_nanf("")};
     }
-    store_one_tile<EPI>([&](int p) { return make_float2(sum[p >> 1][2 * (p & 1)], sum[p >> 1][2 * (p & 1) + 1]); },
+    store_one_tile<EPI, A>([&](int p) { return make_float2(sum[p >> 1][2 * (p & 1)], sum[p >> 1][2 * (p & 1) + 1]); },
                         g, nb, mb, ab >> 2, ab & 3);
   }
   if (tid == 0 &&
@@ -906,7 +920,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   }
 }
 
-inline Args make_args(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
+inline Args make_args(int bn, const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
                       const void* residual, int ldr) {
   Args g;
   g.w = static_cast<const bf16x8_t*>(w);
@@ -918,7 +932,7 @@ inline Args make_args(const void* w, int N, int K, const void* x, int M, int ldx
   g.ldr = ldr;
   g.M = M;
   g.KT = K / kTileK;
-  g.n_blocks = N / BN;
+  g.n_blocks = N / bn;
   g.m_blocks = (M + BM - 1) / BM;
   return g;
 }
@@ -946,11 +960,24 @@ inline void split_plan(int T, int units, int grid, int* R, int* S) {
   *S = s;
 }
 
+// Weight tiles per wave for an N x M problem on `grid` CUs: 192-row blocks
+// (A = 3) when N allows them and they need fewer block-rows of work per CU
+// than 256-row blocks (ceil(blocks / grid) rounds of BN rows each), e.g. QKV
+// (N = 6144) at 2048 tokens: 256 blocks of 192 rows in one round instead of
+// 192 blocks of 256 rows that leave a quarter of the CUs idle.  Ties keep 256.
+inline int choose_tiles(int N, int m_blocks, int grid) {
+  if (N % kBN<3> != 0) return 4;
+  if (N % kBN<4> != 0) return 3;
+  const long r4 = ((long)(N / kBN<4>) * m_blocks + grid - 1) / grid;
+  const long r3 = ((long)(N / kBN<3>) * m_blocks + grid - 1) / grid;
+  return r3 * kBN<3> < r4 * kBN<4> ? 3 : 4;
+}
+
 // `grid` = CUs available to the split (0: no split, no workspace needed).
-template <int EPI>
+template <int EPI, int A>
 hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
                   const void* residual, int ldr, void* workspace, int grid, hipStream_t stream) {
-  const Args g = make_args(w, N, K, x, M, ldx, y, ldy, residual, ldr);
+  const Args g = make_args(kBN<A>, w, N, K, x, M, ldx, y, ldy, residual, ldr);
   const int T = g.n_blocks * g.m_blocks;
   Split k;
   k.units = g.KT / 4;
@@ -962,7 +989,7 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
   k.partials = ws != nullptr ? ws + kSkPartialsOffset : nullptr;
   k.partial_bytes = (unsigned)((size_t)k.R * k.S * kSkPartialBytes);
   k.spin_limit = g_wait_limit.load(std::memory_order_relaxed);
-  gemm_wdx_kernel<EPI><<<dim3(k.dp + k.R * k.S), dim3(kThreads), 0, stream>>>(g, k);
+  gemm_wdx_kernel<EPI, A><<<dim3(k.dp + k.R * k.S), dim3(kThreads), 0, stream>>>(g, k);
   return hipGetLastError();
 }
 
@@ -983,7 +1010,9 @@ hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx
 
 namespace {
 
-bool sk_shape(int M, int N, int K) { return M > kGemmBM && N % wdx::BN == 0 && K % (2 * wdx::BK) == 0; }
+bool sk_shape(int M, int N, int K) {
+  return M > kGemmBM && (N % wdx::kBN<4> == 0 || N % wdx::kBN<3> == 0) && K % (2 * wdx::BK) == 0;
+}
 
 // Workgroups resident at once on `device` (the kernel holds 512 registers
 // per lane, so one per CU), capped by the workspace's flag capacity: the
@@ -998,7 +1027,7 @@ hipError_t sk_grid(int device, int* grid_out) {
     hipError_t err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
     if (err != hipSuccess) return err;
     err = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, reinterpret_cast<const void*>(&wdx::gemm_wdx_kernel<0>), wdx::kThreads, 0);
+        &per_cu, reinterpret_cast<const void*>(&wdx::gemm_wdx_kernel<0, 4>), wdx::kThreads, 0);
     if (err != hipSuccess) return err;
     int grid = cus * (per_cu > 0 ? per_cu : 1);
     cache[device] = grid < kSkMaxGrid ? grid : kSkMaxGrid;
@@ -1037,15 +1066,25 @@ hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M,
       if ((size_t)grid > fit) grid = (int)fit;
     }
     void* ws = grid > 0 ? workspace : nullptr;
-    switch (epi) {
-      case Epilogue::kSiluMul:
-        return wdx::launch<1>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
-      case Epilogue::kResidualAdd:
-        return wdx::launch<2>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
-      case Epilogue::kNone:
-      default:
-        return wdx::launch<0>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
-    }
+    int device = 0, cus = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    err = sk_grid(device, &cus);
+    if (err != hipSuccess) return err;
+    const int tiles = wdx::choose_tiles(N, (M + wdx::BM - 1) / wdx::BM, cus);
+    auto go = [&](auto a_tag) -> hipError_t {
+      constexpr int A = decltype(a_tag)::value;
+      switch (epi) {
+        case Epilogue::kSiluMul:
+          return wdx::launch<1, A>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
+        case Epilogue::kResidualAdd:
+          return wdx::launch<2, A>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
+        case Epilogue::kNone:
+        default:
+          return wdx::launch<0, A>(w, N, K, x, M, ldx, y, ldy, residual, ldr, ws, grid, stream);
+      }
+    };
+    return tiles == 3 ? go(std::integral_constant<int, 3>{}) : go(std::integral_constant<int, 4>{});
   }
   if (M > kGemmBM && N % big::BN == 0 && K % big::BK == 0) {
     switch (epi) {

@@ -380,3 +380,22 @@ def test_split_k_lost_wait_is_reported_and_poisons(gpu):
     torch.cuda.synchronize()
     assert kernels.linear_error(ws) == 0
     assert_parity(y2.cpu(), expect, "split-K after the limit is restored")
+
+
+@pytest.mark.parametrize("m", [1024, 2048])
+def test_prefill_192_row_blocks_with_epilogues(gpu, m):
+    """Shapes whose weight rows split into 192-row blocks (N % 192 == 0 with
+    fewer block-rows per CU than 256-row blocks): the residual epilogue on a
+    QKV-shaped weight, and SiLU*up on a fused gate_up of 2 x 1536 rows, with
+    the split-K workspace (M = 1024: 128 blocks split in two) and without."""
+    n, k = G.qkv_dim, G.hidden_size
+    w = weight(n, k, seed=95)
+    x = activations(m, k, seed=950)
+    r = activations(m, n, seed=951)
+    for ws in ("auto", None):
+        y = _gpu_linear(x, w, epilogue=_lib.EPI_RESIDUAL_ADD, residual=r, workspace=ws)
+        assert_parity(y, r + ref.linear(x, w), f"qkv-shaped + residual M={m} workspace={ws}")
+    inter = 1536
+    wg = weight(2 * inter, k, seed=96)
+    y = _gpu_linear(x, wg, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
+    assert_parity(y, ref.silu_mul(ref.linear(x, wg), inter), f"gate_up 2x{inter} + silu M={m}")
