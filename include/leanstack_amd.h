@@ -106,7 +106,7 @@ int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* 
  *   w_packed   device, layout LSK_LAYOUT_MFMA16X32 (epilogue NONE / RESIDUAL_ADD)
  *              or LSK_LAYOUT_MFMA16X32_GATEUP (epilogue SILU_MUL; N = 2*I)
  *   x          device bf16, row m at x + m*ldx (ldx >= K, ldx % 8 == 0,
- *              16-byte aligned)
+ *              ldx <= 2^22, 16-byte aligned)
  *   y          device bf16, row m at y + m*ldy; N columns, or N/2 for
  *              SILU_MUL (ldy % 4 == 0, 8-byte aligned)
  *   residual   device bf16 [M][N] at stride ldr, RESIDUAL_ADD only (else NULL)

@@ -477,12 +477,14 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 // weight fragments from global memory straight into registers: a packed 1 KB
 // tile already is MFMA operand data in lane order, so a 32-row A fragment is
 // two 512-byte contiguous runs and needs no LDS staging.  Only the
-// activations go through LDS.  Per stage and CU this moves 96 KB through LDS
-// (32 KB activation writes, 64 KB fragment reads) instead of 192 KB; the two
-// waves that share a weight-row half fetch the same lines, the second mostly
-// from L1.  Weight fragments are prefetched one stage ahead into the idle one
-// of two register sets; the stage loop is unrolled by two so the sets swap
-// roles without copies, which requires an even number of stages.
+// activations go through LDS, and they go there by DMA (buffer_load ... lds):
+// no VGPRs and no ds_write instructions, 64 KB of fragment reads per stage
+// and CU.  The two waves that share a weight-row half fetch the same lines,
+// the second mostly from L1.  Weight fragments are prefetched one stage
+// ahead into the idle one of two register sets, activations two stages
+// ahead into the free one of three LDS buffers; the stage loop is unrolled
+// by six so both rotations run without copies, which requires an even
+// number of stages.
 namespace wdx {
 
 constexpr int BN = 256, BM = 256, BK = 64;
@@ -492,22 +494,12 @@ template <int A>
 constexpr int kBN = 64 * A;
 constexpr int kThreads = 256;
 constexpr int kXStageBytes = BM * BK * 2;  // 32 KB of activation fragments per stage
-constexpr int kXChunks = 8;                // 16-byte activation chunks per thread per stage
 
 using big::f32x16_t;
 using big::mfma32;
 using big::kSchedMfma;
 using big::kSchedVmemRead;
 using big::kSchedDsRead;
-using big::kSchedDsWrite;
-
-__device__ __forceinline__ int x_lds_off(int m, int k8) {
-  return ((m >> 5) * 4 + (k8 >> 1)) * 1024 + ((((m & 31) ^ (2 * k8)) + 32 * (k8 & 1)) << 4);
-}
-
-struct XRegs {
-  bf16x8_t v[kXChunks];
-};
 
 template <int A>
 struct WFrags {
@@ -524,23 +516,6 @@ __device__ __forceinline__ void load_w(WFrags<A>& f, const bf16x8_t* __restrict_
     for (int a = 0; a < A; ++a) f.v[q][a] = wl[((size_t)(2 * a) * KT + 2 * s + (q >> 1)) * 64 + (q & 1) * 32];
 }
 
-__device__ __forceinline__ void load_x(XRegs& r, const __bf16* __restrict__ x, int ldx, int M, int m0, int s,
-                                       int tid) {
-#pragma unroll
-  for (int c = 0; c < kXChunks; ++c) {
-    const int u = c * kThreads + tid;
-    r.v[c] = load_x_row(x, ldx, M, m0 + (u >> 3), s * BK + (u & 7) * 8);
-  }
-}
-
-__device__ __forceinline__ void store_x(unsigned char* buf, const XRegs& r, int tid) {
-#pragma unroll
-  for (int c = 0; c < kXChunks; ++c) {
-    const int u = c * kThreads + tid;
-    *reinterpret_cast<bf16x8_t*>(buf + x_lds_off(u >> 3, u & 7)) = r.v[c];
-  }
-}
-
 struct Args {
   const bf16x8_t* w;
   const __bf16* x;
@@ -549,21 +524,62 @@ struct Args {
   int ldx, ldy, ldr, M, KT, n_blocks, m_blocks;
 };
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Activation stage s of block rows m0.. straight into LDS: 256 tokens x 64 K
+// as 128-byte rows, token t's 16-byte chunk c at position c ^ (t & 7) (a
+// conflict-free bank pattern for the B-fragment reads).  One
+// buffer_load_dwordx4 ... lds moves 1 KB = 8 rows: lane l lands at row l >> 3,
+// position l & 7, so it fetches chunk (l & 7) ^ (l >> 3) of its row; the 8
+// lanes of a row still read one whole 128-byte line.  Rows past the last
+// token re-read it (rmax); the buffer covers exactly the block's rows.
+// MUBUF, not FLAT: a FLAT load that writes LDS makes the compiler drain
+// every counter before the next dependent use.
+__device__ __forceinline__ void dma_x(unsigned char* buf, __amdgpu_buffer_rsrc_t rsrc, int ldx, int rmax, int s,
+                                      int wave, int lane) {
+  const int r = lane >> 3;
+  const int c = (lane & 7) ^ r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int j = wave * 8 + i;  // 1 KB block: tokens 8j .. 8j+7
+    const int row = min(8 * j + r, rmax);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(buf + j * 1024), 16, (row * ldx + c * 8) * 2,
+                                             s * BK * 2, 0, 0);
+  }
+}
+
+// The stage barrier: s_waitcnt vmcnt(4A + 8) lgkmcnt(0), then s_barrier.
+// Only the current stage's 4A weight loads and 8 activation DMAs may still
+// be in flight after it, so the previous stage's DMA has landed in every
+// wave.  Not __syncthreads: its release fence waits for vmcnt(0), i.e. for
+// the loads just issued too.  The builtins (not inline asm) let the
+// compiler's wait-counter model see these waits; the empty asm statements
+// keep memory accesses from moving across them.
+template <int A>
+__device__ __forceinline__ void stage_sync() {
+  constexpr int vm = 4 * A + 8;
+  constexpr int imm = (vm & 15) | ((vm >> 4) << 14) | (7 << 4);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(imm);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // acc[a][b] += W rows of 32-row tiles (wn*4 + a) x tokens of 32-token tiles
 // (wm*4 + b) over stages [s0, s1) (s1 - s0 even) of block (nb, mb).
 //
-// Software pipeline over 64-K stages with two LDS activation buffers.  While
-// the MFMAs of stage s run on buffer s&1 with weight fragments wc, the same
-// instruction stream reads the activation fragments of the next 16-K step,
-// loads stage s+1's weight fragments into the idle register set, writes
-// stage s+1's activations (loaded one stage earlier) into buffer (s+1)&1 and
-// issues the activation loads of stage s+2.  The barrier before the last
-// 16-K step publishes buffer (s+1)&1 and retires every read of buffer s&1.
-// Stage indices past s1 are clamped: those loads stay in bounds and the data
-// they stage is never multiplied.
+// Software pipeline over 64-K stages with three LDS activation buffers.
+// While the MFMAs of stage s run on buffer cur with weight fragments wc, the
+// same instruction stream reads the activation fragments of the next 16-K
+// step, loads stage s+1's weight fragments into the idle register set and
+// DMAs stage s+2's activations into the buffer stage s-1 read.  The barrier
+// before the last 16-K step publishes stage s+1's buffer (its DMA was issued
+// one stage earlier) and retires every read of this stage's.  Stage indices
+// past s1 are clamped: those loads stay in bounds and the data they stage is
+// never multiplied.
 template <int A>
-__device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, unsigned char* lds, int nb, int mb,
-                                         int s0, int s1) {
+__device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, unsigned char* xa, unsigned char* xb,
+                                         unsigned char* xc, int nb, int mb, int s0, int s1) {
   // Opaque per call: keeps the per-lane offsets below from being hoisted out
   // of a caller's loop over blocks, where they would stay live (and spill)
   // across the epilogues.
@@ -577,13 +593,16 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, u
   const int li = lane & 31;
   const int kg = lane >> 5;
   const int KT = g.KT;
+  const int rmax = min(g.M - m0, BM) - 1;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(g.x + (size_t)m0 * g.ldx), (short)0, (rmax + 1) * g.ldx * 2, 0x00020000);
 
   // This lane's element of weight fragment (a=0, q=0) at stage 0.
   const bf16x8_t* wl =
       g.w + ((size_t)(nb * (kBN<A> / kTileRows) + wn * 2 * A + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
   int x_lane[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) x_lane[q] = wm * 4 * 4096 + q * 1024 + (((li ^ (4 * q + 2 * kg)) + 32 * kg) << 4);
+  for (int q = 0; q < 4; ++q) x_lane[q] = wm * 16384 + li * 128 + ((((2 * q + kg) ^ (li & 7))) << 4);
 
   auto read_b = [&](bf16x8_t* fb, const unsigned char* buf, int q) {
 #pragma unroll
@@ -596,16 +615,18 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, u
       for (int b = 0; b < 4; ++b) acc[a][b] = mfma32(fa[a], fb[b], acc[a][b]);
   };
 
-  XRegs xr;
   WFrags<A> wf0, wf1;
   bf16x8_t fb0[4], fb1[4];
 
   // Interleave groups per 16-K step: 4A MFMAs with the step's LDS and
   // global traffic.
   constexpr int kM = 4 * A;
-  auto stage = [&](int s, const WFrags<A>& wc, WFrags<A>& wn_) {
-    const unsigned char* cur = lds + (s & 1) * kXStageBytes;
-    unsigned char* nxt = lds + ((s + 1) & 1) * kXStageBytes;
+  // Stage s multiplies buffer cur, DMAs the activations of stage s + 2 into
+  // dst (the buffer stage s - 1 read) and, before its barrier, waits for the
+  // DMA of stage s + 1 (issued one stage earlier; only the 4A weight loads
+  // and 8 DMA of this stage may still be in flight).
+  auto stage = [&](int s, const WFrags<A>& wc, WFrags<A>& wn_, const unsigned char* cur, unsigned char* dst,
+                   const unsigned char* nxt) {
     const int sw = min(s + 1, s1 - 1);
     const int sx = min(s + 2, s1 - 1);
 
@@ -627,7 +648,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, u
 
     __builtin_amdgcn_sched_barrier(0);
     read_b(fb0, cur, 2);
-    store_x(nxt, xr, tid);
+    dma_x(dst, xr, g.ldx, rmax, sx, wave, lane);
     mfma_step(wc.v[1], fb1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -637,28 +658,22 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, u
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
     }
     if constexpr (kM > 12) __builtin_amdgcn_sched_group_barrier(kSchedMfma, kM - 12, 0);
 
     __builtin_amdgcn_sched_barrier(0);
     read_b(fb1, cur, 3);
-    load_x(xr, g.x, g.ldx, g.M, m0, sx, tid);
     mfma_step(wc.v[2], fb0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kM - 8, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kM - 4, 0);
 
-    __syncthreads();
+    // Publishes nxt (stage s + 1's DMA) and retires every read of cur.
+    stage_sync<A>();
     read_b(fb0, nxt, 0);
     mfma_step(wc.v[3], fb1);
 #pragma unroll
@@ -670,18 +685,30 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][4], const Args& g, u
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Every wave is past its last read of either buffer (a previous block's
-  // stages) before the prologue overwrites buffer s0&1.
+  // Every wave is past its last read of the buffers (a previous call's
+  // stages) before the prologue overwrites xa and xb.
   __syncthreads();
-  load_x(xr, g.x, g.ldx, g.M, m0, s0, tid);
+  dma_x(xa, xr, g.ldx, rmax, s0, wave, lane);
+  dma_x(xb, xr, g.ldx, rmax, min(s0 + 1, s1 - 1), wave, lane);
   load_w(wf0, wl, KT, s0);
-  store_x(lds + (s0 & 1) * kXStageBytes, xr, tid);
-  load_x(xr, g.x, g.ldx, g.M, m0, min(s0 + 1, s1 - 1), tid);
-  __syncthreads();
-  read_b(fb0, lds + (s0 & 1) * kXStageBytes, 0);
-  for (int s = s0; s < s1; s += 2) {
-    stage(s, wf0, wf1);
-    stage(s + 1, wf1, wf0);
+  stage_sync<A>();
+  read_b(fb0, xa, 0);
+  int s = s0;
+  for (; s + 6 <= s1; s += 6) {
+    stage(s, wf0, wf1, xa, xc, xb);
+    stage(s + 1, wf1, wf0, xb, xa, xc);
+    stage(s + 2, wf0, wf1, xc, xb, xa);
+    stage(s + 3, wf1, wf0, xa, xc, xb);
+    stage(s + 4, wf0, wf1, xb, xa, xc);
+    stage(s + 5, wf1, wf0, xc, xb, xa);
+  }
+  if (s + 2 <= s1) {
+    stage(s, wf0, wf1, xa, xc, xb);
+    stage(s + 1, wf1, wf0, xb, xa, xc);
+    if (s + 4 <= s1) {
+      stage(s + 2, wf0, wf1, xc, xb, xa);
+      stage(s + 3, wf1, wf0, xa, xc, xb);
+    }
   }
 }
 
@@ -809,7 +836,9 @@ struct Split {
 
 template <int EPI, int A>
 __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kXStageBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char xa[kXStageBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char xb[kXStageBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char xc[kXStageBytes];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   f32x16_t acc[A][4];
@@ -821,8 +850,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
     const int t = k.dp % 8 == 0 ? (b % 8) * (k.dp / 8) + b / 8 : b;
     int nb, mb;
     tile_coords(t, g.n_blocks, g.m_blocks, nb, mb);
-    mainloop(acc, g, lds, nb, mb, 0, g.KT / 2);
+    mainloop(acc, g, xa, xb, xc, nb, mb, 0, g.KT / 2);
     store_tile<EPI, A>(acc, g, nb, mb);
+    // The last stages' activation DMAs (clamped, never read) may still be
+    // writing this workgroup's LDS: let them land before the waves end.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
   }
   // Chunk-major order: all split blocks' chunk 0, then chunk 1, ...
@@ -845,7 +877,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
     tile_coords(k.dp + i, g.n_blocks, g.m_blocks, nb, mb);
   }
   const int u0 = chunk * k.units / k.S, u1 = (chunk + 1) * k.units / k.S;
-  mainloop(acc, g, lds, nb, mb, 2 * u0, 2 * u1);
+  mainloop(acc, g, xa, xb, xc, nb, mb, 2 * u0, 2 * u1);
 
   // Publish this chunk's partial (slot chunk*R + i): quad q of tile (a, b)
   // of thread tid at ((4*(4a+b) + q) * 256 + tid) * 16 bytes, so each store

@@ -83,6 +83,8 @@ int check_linear_args(const void* w_packed, int layout_id, int N, int K, const v
   if (!aligned(w_packed, 16)) return fail(LSK_ERR_INVALID, "packed weights must be 16-byte aligned");
   if (ldx < K || ldx % 8 != 0 || !aligned(x, 16))
     return fail(LSK_ERR_INVALID, "x needs ldx >= K, ldx %% 8 == 0 and 16-byte alignment (ldx=%d, K=%d)", ldx, K);
+  if (ldx > kMaxActivationStride)
+    return fail(LSK_ERR_INVALID, "ldx=%d exceeds the largest activation row stride, %d", ldx, kMaxActivationStride);
   const int n_out = epilogue == LSK_EPI_SILU_MUL ? N / 2 : N;
   if (ldy < n_out || ldy % 4 != 0 || !aligned(y, 8))
     return fail(LSK_ERR_INVALID, "y needs ldy >= %d, ldy %% 4 == 0 and 8-byte alignment (ldy=%d)", n_out, ldy);

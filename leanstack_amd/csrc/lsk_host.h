@@ -21,6 +21,11 @@ constexpr int kTileBytes = kTileRows * kTileK * 2;
 // Largest M served by the decode/verify kernel (the MFMA column count).
 constexpr int kDecodeMaxM = 16;
 
+// Largest activation row stride (elements) of a projection: the prefill
+// kernel reads a 256-row block of x through a buffer descriptor whose byte
+// offsets are 32-bit, so 256 * ldx * 2 must stay below 2^31.
+constexpr int kMaxActivationStride = 1 << 22;
+
 // Decode attention geometry (attention.hip): the rows attended are split into
 // at most kAttnMaxChunks chunks of a multiple of kAttnMinChunkRows rows.
 constexpr int kAttnHeadDim = 128;
