@@ -530,26 +530,30 @@ struct Args {
   __bf16* y;
   const __bf16* residual;
   int ldx, ldy, ldr, M, KT, n_blocks, m_blocks;
+  int wide_io;  // y (and the residual) allow 16-byte row accesses
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Activation stage s of block rows m0.. straight into LDS: 256 tokens x 64 K
-// as 128-byte rows, token t's 16-byte chunk c at position c ^ (t & 7) (a
-// conflict-free bank pattern for the B-fragment reads).  One
-// buffer_load_dwordx4 ... lds moves 1 KB = 8 rows: lane l lands at row l >> 3,
-// position l & 7, so it fetches chunk (l & 7) ^ (l >> 3) of its row; the 8
-// lanes of a row still read one whole 128-byte line.  Rows past the last
-// token re-read it (rmax); the buffer covers exactly the block's rows.
+// as 128-byte rows, token t's 16-byte chunk c at position c ^ f(t) with
+// f(t) = (t ^ (t >> 3)) & 7.  The B-fragment reads (lane li reads one chunk
+// of token li) then hit distinct banks for any 8 consecutive lanes within
+// a 128-byte bank row and for any 16 within a 256-byte one.  One
+// buffer_load_dwordx4 ... lds moves 1 KB = 8 rows (block j = tokens 8j..):
+// lane l lands at row r = l >> 3, position l & 7, so it fetches chunk
+// (l & 7) ^ r ^ (j & 7) of its row; the 8 lanes of a row still read one
+// whole 128-byte line.  Rows past the last token re-read it (rmax); the
+// buffer covers exactly the block's rows.
 // MUBUF, not FLAT: a FLAT load that writes LDS makes the compiler drain
 // every counter before the next dependent use.
 __device__ __forceinline__ void dma_x(unsigned char* buf, __amdgpu_buffer_rsrc_t rsrc, int ldx, int rmax, int s,
                                       int wave, int lane) {
   const int r = lane >> 3;
-  const int c = (lane & 7) ^ r;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int j = wave * 8 + i;  // 1 KB block: tokens 8j .. 8j+7
+    const int j = wave * 8 + i;  // 1 KB block: tokens 8j .. 8j+7 (j & 7 == i)
+    const int c = (lane & 7) ^ r ^ i;
     const int row = min(8 * j + r, rmax);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t*)(buf + j * 1024), 16, (row * ldx + c * 8) * 2,
                                              s * BK * 2, 0, 0);
@@ -621,13 +625,18 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][TB], const Args& g, 
   // This lane's element of weight fragment (a=0, q=0) at stage 0.
   const bf16x8_t* wl =
       g.w + ((size_t)(nb * (kBN<A, TB> / kTileRows) + wn * 2 * A + (li >> 4)) * KT) * 64 + (li & 15) + kg * 16;
+  // Chunk 2q + kg of token t = wm*TB*32 + b*32 + li sits at position
+  // (2q + kg) ^ (li & 7) ^ (li >> 3) ^ 4(b & 1): x_lane[q] holds it for
+  // even b, odd b flip bit 6 of the byte offset.
   int x_lane[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) x_lane[q] = wm * TB * 4096 + li * 128 + ((((2 * q + kg) ^ (li & 7))) << 4);
+  for (int q = 0; q < 4; ++q)
+    x_lane[q] = wm * TB * 4096 + li * 128 + ((((2 * q + kg) ^ (li & 7) ^ (li >> 3))) << 4);
 
   auto read_b = [&](bf16x8_t* fb, const unsigned char* buf, int q) {
 #pragma unroll
-    for (int b = 0; b < TB; ++b) fb[b] = *reinterpret_cast<const bf16x8_t*>(buf + b * 4096 + x_lane[q]);
+    for (int b = 0; b < TB; ++b)
+      fb[b] = *reinterpret_cast<const bf16x8_t*>(buf + b * 4096 + (x_lane[q] ^ ((b & 1) << 6)));
   };
   auto mfma_step = [&](const bf16x8_t* fa, const bf16x8_t* fb) {
 #pragma unroll
@@ -760,6 +769,125 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[A][TB], const A
                                  mb, a, b);
 }
 
+// Epilogue of a whole block through LDS.  Stored straight from the
+// accumulators (store_tile), each store instruction writes 8 bytes per lane
+// into 32 different token rows; every CU does that at the same moment at
+// the end of a round, and it cost 14-19 us of a 2048 x 8192 output.  Here
+// each wave rounds its results to bf16 into its own 16 KB of the (free)
+// activation buffers, token-major, then reads them back 16 bytes per lane
+// in row order, so one store instruction covers whole row segments (8 rows
+// of 128 bytes for the 2x8 wave tile).  Two passes of half the wave's
+// tokens each.  Needs every wave past its last activation read and no DMA
+// in flight (the caller's barrier).  Rounding is that of store_one_tile:
+// bf16 products, then the residual added in fp32 and rounded again.
+//
+// Region layout: token row r of C bytes (C = 64A plain, 32A SiLU*up), its
+// 16-byte chunk c at position c ^ (f(r) mod C/16), f(r) = (r ^ (r >> 3)) & 7
+// (C/16 is 8, 4, 12 or 6: the XOR uses the low 3, 2, 2 or 1 bits so every
+// position stays in the row).
+template <int C>
+__device__ __forceinline__ int epi_pos(int r, int c) {
+  constexpr int kChunks = C / 16;
+  constexpr int kMask = kChunks % 8 == 0 ? 7 : kChunks % 4 == 0 ? 3 : kChunks % 2 == 0 ? 1 : 0;
+  return r * C + ((c ^ ((r ^ (r >> 3)) & kMask)) << 4);
+}
+
+template <int EPI, int A, int TB>
+__device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[A][TB], const Args& g, int nb, int mb,
+                                               unsigned char* xa, unsigned char* xb) {
+  constexpr int WN = TB / 2;
+  constexpr bool kSilu = EPI == static_cast<int>(Epilogue::kSiluMul);
+  constexpr int C = kSilu ? 32 * A : 64 * A;  // output bytes per token of this wave
+  constexpr int HB = TB / 2;                  // token tiles per pass
+  constexpr int kChunks = HB * 32 * C / 16;   // 16-byte chunks per pass
+  static_assert(HB * 32 * C <= 16384, "a pass must fit the wave's 16 KB region");
+  static_assert(kChunks % 64 == 0, "whole chunks per lane");
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wn = wave % WN;
+  const int wm = wave / WN;
+  const int li = lane & 31;
+  const int kg = lane >> 5;
+  unsigned char* reg = (wave < 2 ? xa : xb) + (wave & 1) * 16384;
+  // First output column of this wave and its first token.
+  const int n0 = (nb * WN + wn) * A * (kSilu ? 16 : 32);
+  const int t0 = mb * BM + wm * TB * 32;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int b = 0; b < HB; ++b)
+#pragma unroll
+      for (int a = 0; a < A; ++a) {
+        const f32x16_t& v = acc[a][h * HB + b];
+        const int r = b * 32 + li;
+        if constexpr (kSilu) {
+          // rows 8jj + 4kg + e of the tile are gate, 16 + the same are up
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) {
+            const int col = a * 16 + 8 * jj + 4 * kg;  // intermediate column within the wave
+            unsigned short o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = bf16_bits(silu_mul_bf16(v[4 * jj + e], v[4 * jj + 8 + e]));
+            *reinterpret_cast<u32x2_t*>(reg + epi_pos<C>(r, col >> 3) + (col & 7) * 2) =
+                u32x2_t{o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16)};
+          }
+        } else {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int col = a * 32 + 8 * jj + 4 * kg;
+            *reinterpret_cast<u32x2_t*>(reg + epi_pos<C>(r, col >> 3) + (col & 7) * 2) =
+                u32x2_t{bf16_bits(v[4 * jj]) | ((unsigned)bf16_bits(v[4 * jj + 1]) << 16),
+                        bf16_bits(v[4 * jj + 2]) | ((unsigned)bf16_bits(v[4 * jj + 3]) << 16)};
+          }
+        }
+      }
+    // The same wave reads back what it wrote: LDS executes one wave's
+    // accesses in order.
+#pragma unroll
+    for (int i = 0; i < kChunks / 64; ++i) {
+      const int k = i * 64 + lane;
+      const int r = k / (C / 16);
+      const int c = k % (C / 16);
+      const int m = t0 + h * HB * 32 + r;
+      const u32x4_t q = *reinterpret_cast<const u32x4_t*>(reg + epi_pos<C>(r, c));
+      if (m >= g.M) continue;
+      const int n = n0 + c * 8;
+      __bf16* dst = g.y + (size_t)m * g.ldy + n;
+      if constexpr (EPI == static_cast<int>(Epilogue::kResidualAdd)) {
+        const __bf16* rs = g.residual + (size_t)m * g.ldr + n;
+        u32x4_t rv;
+        if (g.wide_io) {
+          rv = *reinterpret_cast<const u32x4_t*>(rs);
+        } else {
+          const unsigned short* r16 = reinterpret_cast<const unsigned short*>(rs);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rv[e] = r16[2 * e] | ((unsigned)r16[2 * e + 1] << 16);
+        }
+        u32x4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = __builtin_bit_cast(float, q[e] << 16) + __builtin_bit_cast(float, rv[e] << 16);
+          const float hi = __builtin_bit_cast(float, q[e] & 0xffff0000u) + __builtin_bit_cast(float, rv[e] & 0xffff0000u);
+          o[e] = bf16_bits(lo) | ((unsigned)bf16_bits(hi) << 16);
+        }
+        if (g.wide_io) {
+          *reinterpret_cast<u32x4_t*>(dst) = o;
+        } else {
+          reinterpret_cast<u32x2_t*>(dst)[0] = u32x2_t{o[0], o[1]};
+          reinterpret_cast<u32x2_t*>(dst)[1] = u32x2_t{o[2], o[3]};
+        }
+      } else {
+        if (g.wide_io) {
+          *reinterpret_cast<u32x4_t*>(dst) = q;
+        } else {
+          reinterpret_cast<u32x2_t*>(dst)[0] = u32x2_t{q[0], q[1]};
+          reinterpret_cast<u32x2_t*>(dst)[1] = u32x2_t{q[2], q[3]};
+        }
+      }
+    }
+  }
+}
+
 template <int A, int TB>
 __device__ __forceinline__ void zero(f32x16_t (&acc)[A][TB]) {
 #pragma unroll
@@ -844,10 +972,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
     int nb, mb;
     tile_coords(t, g.n_blocks, g.m_blocks, nb, mb);
     mainloop(acc, g, xa, xb, xc, nb, mb, 0, g.KT / 2);
-    store_tile<EPI, A, TB>(acc, g, nb, mb);
     // The last stages' activation DMAs (clamped, never read) may still be
-    // writing this workgroup's LDS: let them land before the waves end.
+    // writing the buffers and other waves may still read them: both end
+    // before the epilogue reuses them.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    store_tile_lds<EPI, A, TB>(acc, g, nb, mb, xa, xb);
     return;
   }
   // Chunk-major order: all split blocks' chunk 0, then chunk 1, ...
@@ -960,6 +1090,8 @@ inline Args make_args(int bn, const void* w, int N, int K, const void* x, int M,
   g.KT = K / kTileK;
   g.n_blocks = N / bn;
   g.m_blocks = (M + BM - 1) / BM;
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  g.wide_io = a16(y) && ldy % 8 == 0 && (residual == nullptr || (a16(residual) && ldr % 8 == 0));
   return g;
 }
 

@@ -399,3 +399,54 @@ def test_prefill_192_row_blocks_with_epilogues(gpu, m):
     wg = weight(2 * inter, k, seed=96)
     y = _gpu_linear(x, wg, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
     assert_parity(y, ref.silu_mul(ref.linear(x, wg), inter), f"gate_up 2x{inter} + silu M={m}")
+
+
+@pytest.mark.parametrize("case", ["plain_2x8", "residual_2x8", "residual_3x4", "silu_3x4", "silu_2x8"])
+@pytest.mark.parametrize("narrow", [False, True])
+def test_prefill_whole_block_epilogue_strides(gpu, case, narrow):
+    """The whole-block prefill epilogue (no workspace: one workgroup per
+    output block) through the C ABI, at contiguous 16-byte-aligned output and
+    residual rows and at the narrowest the ABI accepts: y 8-byte aligned with
+    ldy % 8 == 4, the residual 2-byte aligned with ldr % 8 == 2.  Elements
+    between the rows stay as they were.  M = 300 leaves a partial token block;
+    the 2x8 cases run 256-row weight blocks, the 3x4 cases 192-row ones."""
+    dev = torch.device("cuda:0")
+    m, k = 300, G.hidden_size
+    if case.startswith("silu"):
+        inter = 1536 if case.endswith("3x4") else 2048
+        n, layout, epi = 2 * inter, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL
+        n_out = inter
+    else:
+        n = G.qkv_dim if case.endswith("3x4") else G.hidden_size
+        layout, n_out = _lib.LAYOUT_MFMA16X32, n
+        epi = _lib.EPI_RESIDUAL_ADD if case.startswith("residual") else _lib.EPI_NONE
+    w = weight(n, k, seed=97)
+    x = activations(m, k, seed=970)
+    pw = PackedWeight.from_rowmajor(w.to(dev), layout)
+    xd = x.to(dev)
+    ldy, y_off = (n_out + 4, 4) if narrow else (n_out, 0)
+    y_buf = torch.full((m * ldy + 8,), -7.0, device=dev, dtype=torch.bfloat16)
+    res_ptr, ldr, r = None, 0, None
+    if epi == _lib.EPI_RESIDUAL_ADD:
+        r = activations(m, n, seed=971)
+        ldr, r_off = (n + 2, 1) if narrow else (n, 0)
+        r_buf = torch.zeros((m * ldr + 8,), device=dev, dtype=torch.bfloat16)
+        r_buf[r_off:r_off + m * ldr].view(m, ldr)[:, :n] = r.to(dev)
+        res_ptr = r_buf.data_ptr() + 2 * r_off
+    lib = _lib.load()
+    status = lib.lsk_linear_bf16(pw.data.data_ptr(), layout, n, k, xd.data_ptr(), m, k,
+                                 y_buf.data_ptr() + 2 * y_off, ldy, epi, res_ptr, ldr, None, 0,
+                                 torch.cuda.current_stream().cuda_stream)
+    _lib.check(status, "lsk_linear_bf16")
+    torch.cuda.synchronize()
+    rows = y_buf[y_off:y_off + m * ldy].view(m, ldy).cpu()
+    y = rows[:, :n_out]
+    if epi == _lib.EPI_SILU_MUL:
+        expect = ref.silu_mul(ref.linear(x, w), n_out)
+    elif epi == _lib.EPI_RESIDUAL_ADD:
+        expect = r + ref.linear(x, w)
+    else:
+        expect = ref.linear(x, w)
+    assert_parity(y, expect, f"{case} narrow={narrow}")
+    untouched = torch.cat([y_buf[:y_off].cpu(), rows[:, n_out:].reshape(-1), y_buf[y_off + m * ldy:].cpu()])
+    assert bool((untouched == -7.0).all()), "the epilogue wrote outside the output rows"
