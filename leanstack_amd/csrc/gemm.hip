@@ -1002,6 +1002,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   const int u0 = chunk * k.units / k.S, u1 = (chunk + 1) * k.units / k.S;
   mainloop(acc, g, xa, xb, xc, nb, mb, 2 * u0, 2 * u1);
 
+  // This workgroup sums tiles [ab0, ab1) of the block (each thread its own
+  // quads of them); it keeps its partial of those in its accumulators and
+  // publishes only the others.
+  const int ab0 = chunk * A * TB / k.S, ab1 = (chunk + 1) * A * TB / k.S;
   // Publish this chunk's partial (slot chunk*R + i): quad q of tile (a, b)
   // of thread tid at ((4*(TB*a+b) + q) * 256 + tid) * 16 bytes, so each store
   // instruction writes 1 KB contiguously straight from four accumulators.
@@ -1011,15 +1015,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
 #pragma unroll
     for (int a = 0; a < A; ++a)
 #pragma unroll
-      for (int bb = 0; bb < TB; ++bb)
+      for (int bb = 0; bb < TB; ++bb) {
+        const int ab = a * TB + bb;
+        if (ab >= ab0 && ab < ab1) continue;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           f32x4_t v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[e]) : "a"(acc[a][bb][4 * q + e]));
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), parts, tid * 16,
-                                                 slot + ((a * TB + bb) * 4 + q) * kThreads * 16, kCoherent);
+                                                 slot + (ab * 4 + q) * kThreads * 16, kCoherent);
         }
+      }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -1042,33 +1049,46 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   __syncthreads();
   const bool poison = gave_up != 0;
 
-  // Sum this workgroup's share of the block's tiles over the S chunks.
+  // Sum this workgroup's share of the block's tiles over the S chunks, in
+  // chunk order, its own chunk's partial from its accumulators.
   const unsigned first = (unsigned)i * (unsigned)kSkPartialBytes;
   const unsigned chunk_stride = (unsigned)k.R * (unsigned)kSkPartialBytes;
-  const int ab1 = (chunk + 1) * A * TB / k.S;
-  for (int ab = chunk * A * TB / k.S; ab < ab1; ++ab) {
-    f32x4_t sum[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < k.S; ++c) {
-      f32x4_t v[4];
+  for (int a = 0; a < A; ++a)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        v[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                               parts, tid * 16, first + c * chunk_stride + (ab * 4 + q) * kThreads * 16,
-                                               kCoherent));
+    for (int bb = 0; bb < TB; ++bb) {
+      const int ab = a * TB + bb;
+      if (ab < ab0 || ab >= ab1) continue;
+      f32x4_t sum[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sum[q] += v[q];
+      for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < k.S; ++c) {
+        f32x4_t v[4];
+        if (c == chunk) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[q][e]) : "a"(acc[a][bb][4 * q + e]));
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            v[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   parts, tid * 16, first + c * chunk_stride + (ab * 4 + q) * kThreads * 16,
+                                                   kCoherent));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum[q] += v[q];
+      }
+      if (poison) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                                                     __builtin_nanf("")};
+      }
+      store_one_tile<EPI, A, TB>(
+          [&](int p) { return make_float2(sum[p >> 1][2 * (p & 1)], sum[p >> 1][2 * (p & 1) + 1]); }, g, nb, mb, a,
+          bb);
     }
-    if (poison) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
-                                                   __builtin_nanf("")};
-    }
-    store_one_tile<EPI, A, TB>(
-        [&](int p) { return make_float2(sum[p >> 1][2 * (p & 1)], sum[p >> 1][2 * (p & 1) + 1]); }, g, nb, mb,
-        ab / TB, ab % TB);
-  }
   if (tid == 0 &&
       __hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)k.S - 1) {
     __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
