@@ -71,13 +71,32 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def profiled_mfma_util() -> dict | None:
-    """MfmaUtil per prefill projection at M = 2048 as the committed counter
-    profile measured it (profiles/prefill_counters.json), or None."""
+def prefill_profile() -> dict:
+    """The committed prefill counter profile (profiles/prefill_counters.json),
+    or {} when absent."""
     path = REPO / "profiles" / "prefill_counters.json"
-    if not path.exists():
+    return json.loads(path.read_text()) if path.exists() else {}
+
+
+def profiled_mfma_util() -> float | None:
+    """Time-weighted MfmaUtil of the four prefill projections at M = 2048 as
+    the committed counter profile measured it, or None."""
+    return prefill_profile().get("mfma_util_pct_m2048")
+
+
+def loaded_clock_peak_tflops(m: int) -> dict | None:
+    """Dense BF16 MFMA peak at the shader clock the committed profile measured
+    under this prefill load (GRBM_GUI_ACTIVE / duration, time-weighted over
+    the four projections at M = m): 256 CUs x 4 SIMDs x 1024 FLOP/clk x f.
+    The published 2.5 PFLOP/s assumes 2.4 GHz; the chip holds less under
+    sustained MFMA load."""
+    prof = prefill_profile()
+    clocks = prof.get(f"clock_ghz_m{m}")
+    weights = prof.get(f"us_m{m}")
+    if not clocks or not weights:
         return None
-    return json.loads(path.read_text()).get("mfma_util_pct_m2048")
+    ghz = sum(clocks[k] * weights[k] for k in clocks) / sum(weights[k] for k in clocks)
+    return {"clock_ghz": round(ghz, 3), "peak": round(256 * 4 * 1024 * ghz * 1e9 / 1e12, 1)}
 
 
 def measured_traffic(kernel_label: str):
@@ -399,6 +418,11 @@ def main() -> int:
             "mfma_util_pct": profiled_mfma_util(),
             "mfma_util_source": "profiles/prefill_gemm_counters.md (rocprofv3 --pmc MfmaUtil, bench.py --pmc-prefill)",
         }
+        loaded = loaded_clock_peak_tflops(2048)
+        if loaded is not None:
+            prefill_roofline["peak_at_loaded_clock"] = loaded["peak"]
+            prefill_roofline["loaded_clock_ghz"] = loaded["clock_ghz"]
+            prefill_roofline["frac_at_loaded_clock"] = round(achieved_tf / loaded["peak"], 4)
 
     cpu = None
     if not args.quick:
@@ -445,6 +469,8 @@ def main() -> int:
             "step_path": "persistent stack kernel" if persistent_is_faster else "HIP graph of 144 projection launches",
             "verify_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in headline.items()},
             "verify_ratio_vs_m1": {str(m): round(v / headline[1], 4) for m, v in headline.items()},
+            # one layer = the step over 36 distinct layers (7.27 GB, no MALL reuse) / 36
+            "one_layer_us": {str(m): round(v * 1e3 / G.num_hidden_layers, 2) for m, v in headline.items()},
             "launches_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep_launches.items()},
             "persistent_sweep_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep.items()},
             "step_with_rmsnorms_us": {str(m): v for m, v in norm_steps.items()},
