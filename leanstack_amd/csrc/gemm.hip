@@ -500,6 +500,7 @@ template <int A, int TB>
 constexpr int kBN = 16 * A * TB;
 constexpr int kRowsWide = kBN<2, 8>;  // 256
 constexpr int kRows192 = kBN<3, 4>;
+constexpr int kRows128 = kBN<1, 8>;   // every wave 32 rows over all 256 tokens
 constexpr int kThreads = 256;
 constexpr int kXStageBytes = BM * BK * 2;  // 32 KB of activation fragments per stage
 
@@ -1138,17 +1139,36 @@ inline void split_plan(int T, int units, int grid, int* R, int* S) {
   *S = s;
 }
 
-// Block height for an N x M problem on `grid` CUs: 3 = 192-row blocks when
-// N allows them and they need fewer block-rows of work per CU than 256-row
-// blocks (4; ceil(blocks / grid) rounds of BN rows each), e.g. QKV
-// (N = 6144) at 2048 tokens: 256 blocks of 192 rows in one round instead of
-// 192 blocks of 256 rows that leave a quarter of the CUs idle.  Ties keep 256.
-inline int choose_tiles(int N, int m_blocks, int grid) {
-  if (N % kRows192 != 0) return 4;
-  if (N % kRowsWide != 0) return 3;
-  const long r4 = ((long)(N / kRowsWide) * m_blocks + grid - 1) / grid;
-  const long r3 = ((long)(N / kRows192) * m_blocks + grid - 1) / grid;
-  return r3 * kRows192 < r4 * kRowsWide ? 3 : 4;
+// Block height for an N x M problem on `grid` CUs, as the 32-row weight
+// tiles per wave A of the wave tile: 3 = 192-row blocks when N allows them
+// and they need fewer block-rows of work per CU than 256-row blocks (4;
+// ceil(blocks / grid) rounds of BN rows each), e.g. QKV (N = 6144) at 2048
+// tokens: 256 blocks of 192 rows in one round instead of 192 blocks of 256
+// rows that leave a quarter of the CUs idle.  Ties keep 256.  Then 1 =
+// 128-row blocks when that choice would split every block at least four
+// ways over `split_grid` CUs (0: no split): half-height blocks halve each
+// split workgroup's fp32 partial and need fewer chunks.  At 512 tokens:
+// o_proj 29.5 -> 23.9 us, QKV 32.2 -> 28.9, down_proj 45.4 -> 41.2; where
+// the blocks split fewer ways (every shape at 2048 tokens) or not at all
+// (gate_up at 512) 128-row blocks measured slower.
+inline int choose_tiles(int N, int m_blocks, int grid, int units, int split_grid) {
+  int a = 4;
+  if (N % kRows192 != 0) {
+    a = 4;
+  } else if (N % kRowsWide != 0) {
+    a = 3;
+  } else {
+    const long r4 = ((long)(N / kRowsWide) * m_blocks + grid - 1) / grid;
+    const long r3 = ((long)(N / kRows192) * m_blocks + grid - 1) / grid;
+    a = r3 * kRows192 < r4 * kRowsWide ? 3 : 4;
+  }
+  if (split_grid > 0 && N % kRows128 == 0) {
+    const int T = (N / (a == 3 ? kRows192 : kRowsWide)) * m_blocks;
+    int R = 0, S = 1;
+    split_plan(T, units, split_grid, &R, &S);
+    if (T < split_grid && S >= 4) return 1;
+  }
+  return a;
 }
 
 // `grid` = CUs available to the split (0: no split, no workspace needed).
@@ -1249,7 +1269,7 @@ hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M,
     if (err != hipSuccess) return err;
     err = sk_grid(device, &cus);
     if (err != hipSuccess) return err;
-    const int tiles = wdx::choose_tiles(N, (M + wdx::BM - 1) / wdx::BM, cus);
+    const int tiles = wdx::choose_tiles(N, (M + wdx::BM - 1) / wdx::BM, cus, K / kTileK / 4, grid);
     auto go = [&](auto a_tag, auto tb_tag) -> hipError_t {
       constexpr int A = decltype(a_tag)::value;
       constexpr int TB = decltype(tb_tag)::value;
@@ -1267,6 +1287,7 @@ hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M,
     // tokens, so each weight fragment is fetched by one wave only (4-9 %
     // faster than (4, 4), whose wave pairs fetched every weight line twice).
     if (tiles == 3) return go(std::integral_constant<int, 3>{}, std::integral_constant<int, 4>{});
+    if (tiles == 1) return go(std::integral_constant<int, 1>{}, std::integral_constant<int, 8>{});
     return go(std::integral_constant<int, 2>{}, std::integral_constant<int, 8>{});
   }
   if (M > kGemmBM && N % big::BN == 0 && K % big::BK == 0) {
