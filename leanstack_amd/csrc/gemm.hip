@@ -64,21 +64,6 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float bf16_round(float v) {
-  return static_cast<float>(static_cast<__bf16>(v));
-}
-
-__device__ __forceinline__ unsigned short bf16_bits(float v) {
-  return __builtin_bit_cast(unsigned short, static_cast<__bf16>(v));
-}
-
-__device__ __forceinline__ float silu_mul_bf16(float g_acc, float u_acc) {
-  const float g = bf16_round(g_acc);
-  const float u = bf16_round(u_acc);
-  const float s = bf16_round(g / (1.0f + expf(-g)));
-  return bf16_round(s * u);
-}
-
 // Block order.  Workgroup b runs on XCD b % 8 (round-robin dispatch), so each
 // XCD gets a contiguous run of the logical order; inside it, tiles go in
 // groups of kGroupM token blocks, all weight blocks of a group before the next

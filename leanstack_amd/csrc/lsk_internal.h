@@ -46,6 +46,35 @@ __host__ __device__ constexpr size_t kStackWsBytes(int count, int G) {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
+// Device arithmetic shared by the kernel translation units.
+
+__device__ __forceinline__ float bf16_round(float v) { return static_cast<float>(static_cast<__bf16>(v)); }
+
+__device__ __forceinline__ unsigned short bf16_bits(float v) {
+  return __builtin_bit_cast(unsigned short, static_cast<__bf16>(v));
+}
+
+// SiLU(g) * u with the rounding chain of the reference: the gate_up product is
+// a bf16 tensor, F.silu returns bf16, and the product is rounded to bf16
+// (src/leanstack/runtime/qwen_explicit.py:828-830, :942-948).  sigmoid(g) =
+// 1 / (1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal (v_exp_f32,
+// v_rcp_f32, 1 ulp each): with the rounding of -g log2 e the float32 result
+// is within ~2^-17 relative of the exact one for |g| < 88.7, far inside the
+// 2^-9 half-ulp of the bf16 it is rounded to, so the two differ by one bf16
+// ulp only where the exact value lies that close to a rounding boundary.
+// v_rcp_f32 flushes a subnormal result, so a denominator above 2^96 (g below
+// -66.5) is scaled by 2^-32 before it and the quotient by 2^-32 after.
+// Below g = -88.7, exp(-g) overflows float32 and the result is -0, as the
+// float32 formula g / (1 + exp(-g)) gives there.
+__device__ __forceinline__ float silu_mul_bf16(float g_acc, float u_acc) {
+  const float g = bf16_round(g_acc);
+  const float u = bf16_round(u_acc);
+  const float d = 1.0f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  const float sc = d > 0x1p96f ? 0x1p-32f : 1.0f;
+  const float s = bf16_round(sc * (g * __builtin_amdgcn_rcpf(d * sc)));
+  return bf16_round(s * u);
+}
+
 // One projection of a stack program, as the kernel reads it (64 bytes).
 struct StackDesc {
   const bf16x8_t* w;

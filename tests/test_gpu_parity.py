@@ -117,6 +117,56 @@ def test_prefill_gate_up_silu(gpu, m):
     assert_parity(y, expect, f"gate_up+silu prefill M={m}")
 
 
+def _every_bf16_gate(rows: int, cols: int) -> torch.Tensor:
+    """[rows, cols] bf16 holding each of the 65536 bit patterns once, the
+    non-finite ones (exponent 0xFF) replaced by 0."""
+    pat = np.arange(rows * cols, dtype=np.uint32).astype(np.uint16)
+    pat[(pat & 0x7F80) == 0x7F80] = 0
+    return torch.from_numpy(pat.reshape(rows, cols).view(np.int16)).view(torch.bfloat16)
+
+
+def _assert_silu_elementwise(got: torch.Tensor, expect: torch.Tensor, what: str) -> None:
+    """Within one bf16 ulp everywhere, identical in at least 99.9 % of the
+    elements: the kernel's float32 SiLU differs from the oracle's by far less
+    than the bf16 half-ulp, so the roundings part only next to a boundary."""
+    g = got.double().numpy()
+    e = expect.double().numpy()
+    ulp = brute.bf16_ulp(np.maximum(np.abs(g), np.abs(e)))
+    bad = np.abs(g - e) > ulp
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements off by more than one ulp, first {np.argwhere(bad)[:4]}"
+    same = float(np.mean(g == e))
+    assert same >= 0.999, f"{what}: only {same:.5f} identical"
+
+
+def test_prefill_silu_every_bf16_gate(gpu):
+    """One-hot activations make gate and up exact weight entries, so the
+    SiLU*up epilogue of the prefill kernel meets every finite bf16 gate value
+    (M = 2048 tokens cycling over K = 128 columns of 512 gate rows)."""
+    inter, k, m = 512, 128, 2048
+    gen = torch.Generator(device="cpu").manual_seed(70)
+    up = (torch.rand((inter, k), generator=gen) * 2 - 1).to(torch.bfloat16)
+    w = torch.cat((_every_bf16_gate(inter, k), up))
+    x = torch.eye(k, dtype=torch.bfloat16).repeat(m // k, 1)
+    y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
+    # gate_up[t] = w[:, t % k] exactly (the CPU bf16 matmul would flush the
+    # subnormal entries, which the MFMA keeps).
+    gate_up = w.t().repeat(m // k, 1)
+    _assert_silu_elementwise(y, ref.silu_mul(gate_up, inter), "prefill SiLU over every bf16 gate")
+
+
+def test_decode_silu_every_bf16_gate(gpu):
+    """The decode kernels' SiLU*up epilogue over every finite bf16 gate value:
+    M = 8 one-hot tokens read columns 0..7 of 8192 gate rows."""
+    inter, k, m = 8192, G.hidden_size, 8
+    gen = torch.Generator(device="cpu").manual_seed(71)
+    w = torch.zeros((2 * inter, k), dtype=torch.bfloat16)
+    w[:inter, :m] = _every_bf16_gate(inter, m)
+    w[inter:, :m] = (torch.rand((inter, m), generator=gen) * 2 - 1).to(torch.bfloat16)
+    x = torch.eye(m, k, dtype=torch.bfloat16)
+    y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
+    _assert_silu_elementwise(y, ref.silu_mul(w[:, :m].t().contiguous(), inter), "decode SiLU over every bf16 gate")
+
+
 def test_prefill_residual(gpu):
     m, n, k = 200, G.hidden_size, G.q_dim
     w = weight(n, k, seed=60)

@@ -117,6 +117,30 @@ def test_silu_mul_applies_silu_to_the_gate_half():
     assert not torch.equal(swapped, out.to(torch.bfloat16))
 
 
+def test_silu_over_every_bf16_gate():
+    """The oracle's SiLU*up (F.silu on bf16, computed in float32) against the
+    float64 chain for every finite bf16 gate and a few up values: within one
+    bf16 ulp and identical almost everywhere, except below g = -88.72, where
+    exp(-g) overflows float32 and the float32 formula gives -0 while the
+    float64 one still gives a value below 2^-121."""
+    pat = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    pat = pat[(pat & 0x7F80) != 0x7F80]
+    g = brute.bf16_bits_to_f64(pat)
+    for u_val in (1.0, -0.75, 0.3125):
+        u = np.full_like(g, u_val)
+        gate = torch.from_numpy(pat.view(np.int16)).view(torch.bfloat16).view(1, -1)
+        up = torch.full_like(gate, u_val)
+        out = ref.silu_mul(torch.cat((gate, up), dim=-1), gate.shape[-1]).double().numpy()[0]
+        with np.errstate(over="ignore"):
+            expect = brute.silu_mul_chain(g, u)
+        overflow = g < -88.72
+        assert np.all(out[overflow] == 0.0)
+        assert np.all(np.abs(expect[overflow]) < 2.0 ** -121)
+        o, e = out[~overflow], expect[~overflow]
+        assert np.all(np.abs(o - e) <= brute.bf16_ulp(np.maximum(np.abs(o), np.abs(e))))
+        assert np.mean(o == e) >= 0.999
+
+
 def test_silu_matches_closed_form_elementwise():
     rng = np.random.default_rng(8)
     g = brute.round_bf16(rng.standard_normal(4096) * 4)
