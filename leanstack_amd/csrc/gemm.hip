@@ -897,8 +897,8 @@ __device__ __forceinline__ void zero(f32x16_t (&acc)[A][TB]) {
 // share lines the same way.  The S workgroups of a split block each store
 // their fp32 accumulators to a workspace slot and count themselves in the
 // block's arrival word; once all S have arrived, workgroup s sums tiles
-// [16s/S, 16(s+1)/S) of the block over the S slots in chunk order and
-// stores them with the epilogue, then counts itself out; the last one out
+// [16s/S, 16(s+1)/S) of the block, its own partial first and then the other
+// S - 1 slots in chunk order, and stores them with the epilogue, then counts itself out; the last one out
 // clears both words.  R*S <= G, and whole-K blocks never wait, so every
 // split workgroup gets a CU.  That holds only while no other kernel shares
 // the device, so the waits are bounded: a workgroup that gives up (after
@@ -1035,8 +1035,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
   __syncthreads();
   const bool poison = gave_up != 0;
 
-  // Sum this workgroup's share of the block's tiles over the S chunks, in
-  // chunk order, its own chunk's partial from its accumulators.
+  // Sum this workgroup's share of the block's tiles over the S chunks: its
+  // own chunk's partial (from its accumulators) first, then the other chunks
+  // in chunk order, three chunks' loads in flight at a time (one round trip
+  // per tile for S <= 4).  Loads past the last chunk put their offset beyond
+  // the partials in the VGPR offset, which the buffer range check covers, and
+  // return zeros without a memory access.
   const unsigned first = (unsigned)i * (unsigned)kSkPartialBytes;
   const unsigned chunk_stride = (unsigned)k.R * (unsigned)kSkPartialBytes;
 #pragma unroll
@@ -1047,24 +1051,26 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_wdx_kernel(Args g, Split k) 
       if (ab < ab0 || ab >= ab1) continue;
       f32x4_t sum[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) sum[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      for (int c = 0; c < k.S; ++c) {
-        f32x4_t v[4];
-        if (c == chunk) {
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
+        for (int e = 0; e < 4; ++e) asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(sum[q][e]) : "a"(acc[a][bb][4 * q + e]));
+      for (int j0 = 0; j0 < k.S - 1; j0 += 3) {
+        f32x4_t v[3][4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v[q][e]) : "a"(acc[a][bb][4 * q + e]));
-        } else {
+        for (int g3 = 0; g3 < 3; ++g3) {
+          const int j = j0 + g3;
+          const int c = j < chunk ? j : j + 1;
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v[q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   parts, tid * 16, first + c * chunk_stride + (ab * 4 + q) * kThreads * 16,
-                                                   kCoherent));
+          for (int q = 0; q < 4; ++q) {
+            const unsigned off = j < k.S - 1 ? first + c * chunk_stride + (ab * 4 + q) * kThreads * 16 : 0x80000000u;
+            v[g3][q] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(parts, off + tid * 16, 0,
+                                                                                          kCoherent));
+          }
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sum[q] += v[q];
+        for (int g3 = 0; g3 < 3; ++g3)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) sum[q] += v[g3][q];
       }
       if (poison) {
 #pragma unroll
