@@ -102,6 +102,16 @@ int lsk_pack_bf16(const void* w_rowmajor_host, int N, int K, int layout_id, void
 /* Inverse of lsk_pack_bf16 (out_rowmajor_host receives W[N][K]). */
 int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* out_rowmajor_host);
 
+/* How lsk_linear_bf16 runs M rows of an [N, K] weight on the current device
+ * with a workspace of ws_bytes (0: none): plan[0] = weight rows per output
+ * block of the prefill block GEMM (256, 192 or 128), plan[1] = output blocks,
+ * plan[2] = blocks whose K range is split over several workgroups, plan[3] =
+ * workgroups (K chunks) per split block (1: no split).  plan = {0, 0, 0, 1}
+ * when the call takes the decode kernels (M <= 16, or a shape off the block
+ * GEMM's tile grid) or the plain 128-row GEMM.  For tests and tuning; no
+ * counterpart in the reference, whose F.linear hides its cuBLAS plan. */
+int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int plan[4]);
+
 /* y[M][*] = epilogue(x[M][K] . W[N][K]^T), bf16 in and out, fp32 accumulate.
  *   w_packed   device, layout LSK_LAYOUT_MFMA16X32 (epilogue NONE / RESIDUAL_ADD)
  *              or LSK_LAYOUT_MFMA16X32_GATEUP (epilogue SILU_MUL; N = 2*I)

@@ -51,6 +51,7 @@ _SIGNATURES: dict[str, tuple[type | None, list]] = {
     "lsk_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "lsk_pack_bf16": (_c_int, [_c_void, _c_int, _c_int, _c_int, _c_void]),
     "lsk_unpack_bf16": (_c_int, [_c_void, _c_int, _c_int, _c_int, _c_void]),
+    "lsk_linear_plan": (_c_int, [_c_int, _c_int, _c_int, _c_size, ctypes.POINTER(_c_int)]),
     "lsk_linear_bf16": (
         _c_int,
         [_c_void, _c_int, _c_int, _c_int, _c_void, _c_int, _c_int, _c_void, _c_int, _c_int, _c_void, _c_int,

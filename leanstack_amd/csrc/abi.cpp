@@ -69,6 +69,22 @@ size_t lsk_workspace_bytes(int op, int M, int N, int K) {
   return 0;
 }
 
+int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int* plan) {
+  lsk::clear_error();
+  if (plan == nullptr) return fail(LSK_ERR_INVALID, "plan is NULL");
+  if (M < 1 || N < 1 || K < 1) return fail(LSK_ERR_INVALID, "M=%d, N=%d, K=%d must be positive", M, N, K);
+  plan[0] = 0;
+  plan[1] = 0;
+  plan[2] = 0;
+  plan[3] = 1;
+  // The routing of lsk_linear_bf16: decode kernels up to kDecodeMaxM rows and
+  // off the GEMM tile grid, the block GEMM otherwise.
+  if (M <= lsk::kDecodeMaxM || N % lsk::kGemmBN != 0 || K % lsk::kGemmBK != 0) return LSK_OK;
+  const hipError_t err = lsk::plan_gemm_linear(M, N, K, ws_bytes, plan);
+  if (err != hipSuccess) return hip_fail(err, "prefill plan");
+  return LSK_OK;
+}
+
 int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const void* x, int M, int ldx, void* y,
                     int ldy, int epilogue, const void* residual, int ldr, void* workspace, size_t ws_bytes,
                     void* hip_stream) {

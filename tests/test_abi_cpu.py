@@ -284,3 +284,18 @@ def test_noalloc_lm_head_rejects_before_launch():
     assert call(layout=2) == _lib.ERR_LAYOUT
     assert call(mode=7) == _lib.ERR_INVALID
     assert call(out=FAKE + 4) == _lib.ERR_INVALID
+
+
+def test_linear_plan_rejects_and_routes_without_a_device():
+    """lsk_linear_plan validates before any HIP call; decode-routed shapes
+    (M <= 16, or off the block GEMM's tile grid) answer {0, 0, 0, 1} on the
+    host alone."""
+    lib = _lib.load()
+    plan = (ctypes.c_int * 4)(9, 9, 9, 9)
+    assert lib.lsk_linear_plan(2048, 2560, 4096, 0, None) == _lib.ERR_INVALID
+    assert lib.lsk_linear_plan(0, 2560, 4096, 0, plan) == _lib.ERR_INVALID
+    assert lib.lsk_linear_plan(64, 2560, -1, 0, plan) == _lib.ERR_INVALID
+    for m, n, k in [(1, 2560, 4096), (16, 19456, 2560), (300, 2560 + 16, 4096), (300, 2560, 4096 + 32)]:
+        plan = (ctypes.c_int * 4)(9, 9, 9, 9)
+        assert lib.lsk_linear_plan(m, n, k, 1 << 26, plan) == _lib.OK
+        assert list(plan) == [0, 0, 0, 1], (m, n, k, list(plan))

@@ -7,6 +7,7 @@ calls the C ABI through leanstack_amd.kernels.
 
 from __future__ import annotations
 
+import ctypes
 import numpy as np
 import pytest
 import torch
@@ -165,6 +166,56 @@ def test_decode_silu_every_bf16_gate(gpu):
     x = torch.eye(m, k, dtype=torch.bfloat16)
     y = _gpu_linear(x, w, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL)
     _assert_silu_elementwise(y, ref.silu_mul(w[:, :m].t().contiguous(), inter), "decode SiLU over every bf16 gate")
+
+
+def _linear_plan(m: int, n: int, k: int) -> list[int]:
+    """The prefill GEMM's plan with the auto workspace: [block rows, blocks,
+    split blocks, chunks per split block]."""
+    lib = _lib.load()
+    plan = (ctypes.c_int * 4)()
+    ws = lib.lsk_workspace_bytes(_lib.OP_LINEAR, m, n, k)
+    assert lib.lsk_linear_plan(m, n, k, ws, plan) == _lib.OK
+    return list(plan)
+
+
+# (M, N, K, epilogue) and the plan each gives on a 256-CU MI355X: the split
+# counts S = 2, 3, 4, 8 and 16 of the last round, 128- and 256-row blocks,
+# each epilogue through the split combine.
+SPLIT_CASES = {
+    "s2": (512, 6144, 2560, _lib.EPI_NONE, [128, 96, 96, 2]),
+    "s3": (1024, 2560, 2560, _lib.EPI_NONE, [128, 80, 80, 3]),
+    "s3_silu": (1024, 2560, 2560, _lib.EPI_SILU_MUL, [128, 80, 80, 3]),
+    "s3_256": (2048, 2560, 4096, _lib.EPI_RESIDUAL_ADD, [256, 80, 80, 3]),
+    "s4": (300, 2560, 9728, _lib.EPI_NONE, [128, 40, 40, 4]),
+    "s8": (200, 2560, 4096, _lib.EPI_RESIDUAL_ADD, [128, 20, 20, 8]),
+    "s16": (200, 1024, 8192, _lib.EPI_NONE, [128, 8, 8, 16]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SPLIT_CASES))
+def test_prefill_every_split_count(gpu, case):
+    """Every split count of the partial last round against the oracle, twice
+    (bitwise equal), with the workspace left zeroed and its error word clear."""
+    m, n, k, epi, plan = SPLIT_CASES[case]
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert _linear_plan(m, n, k) == plan
+    layout = _lib.LAYOUT_MFMA16X32_GATEUP if epi == _lib.EPI_SILU_MUL else _lib.LAYOUT_MFMA16X32
+    w = weight(n, k, seed=80 + k % 97)
+    x = activations(m, k, seed=800 + m)
+    r = activations(m, n, seed=801 + m) if epi == _lib.EPI_RESIDUAL_ADD else None
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(w.to(dev), layout)
+    ws = kernels.prefill_workspace(dev, m, n, k)
+    xd, rd = x.to(dev), (r.to(dev) if r is not None else None)
+    y1 = kernels.linear(xd, pw, epilogue=epi, residual=rd, workspace=ws)
+    y2 = kernels.linear(xd, pw, epilogue=epi, residual=rd, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    assert kernels.linear_error(ws) == 0
+    assert int(ws.view(torch.int32)[64:2048].abs().sum()) == 0  # arrival/departure words zero again
+    yl = ref.linear(x, w)
+    expect = ref.silu_mul(yl, n // 2) if epi == _lib.EPI_SILU_MUL else (r + yl if r is not None else yl)
+    assert_parity(y1.cpu(), expect, f"split-K {case} M={m} N={n} K={k}")
 
 
 def test_prefill_residual(gpu):
