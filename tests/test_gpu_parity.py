@@ -218,6 +218,24 @@ def test_prefill_every_split_count(gpu, case):
     assert_parity(y1.cpu(), expect, f"split-K {case} M={m} N={n} K={k}")
 
 
+@pytest.mark.parametrize("m", [1500, 2047])
+@pytest.mark.parametrize("proj", ["qkv", "down_residual"])
+def test_prefill_ragged_token_count(gpu, m, proj):
+    """Token counts that leave the last 256-token block part-full (220 and
+    255 rows), in full against the oracle: QKV on 192-row blocks in one round,
+    down + residual on split blocks (2 chunks at 1500 tokens, 3 at 2047)."""
+    if proj == "qkv":
+        n, k, epi = G.qkv_dim, G.hidden_size, _lib.EPI_NONE
+    else:
+        n, k, epi = G.hidden_size, G.intermediate_size, _lib.EPI_RESIDUAL_ADD
+    w = weight(n, k, seed=90 + m % 7)
+    x = activations(m, k, seed=900 + m)
+    r = activations(m, n, seed=901 + m) if epi == _lib.EPI_RESIDUAL_ADD else None
+    y = _gpu_linear(x, w, epilogue=epi, residual=r)
+    expect = ref.linear(x, w) if r is None else r + ref.linear(x, w)
+    assert_parity(y, expect, f"{proj} prefill M={m}")
+
+
 def test_prefill_residual(gpu):
     m, n, k = 200, G.hidden_size, G.q_dim
     w = weight(n, k, seed=60)
