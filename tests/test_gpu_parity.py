@@ -440,6 +440,53 @@ def test_prefill_m8192_sampled_rows(gpu, name):
     assert_parity(y[rows], _oracle(x[rows], w, epi), f"{name} prefill M=8192 (rows sampled)")
 
 
+def _random_shapes(count: int, seed: int) -> list[tuple[int, int, int, int]]:
+    """(M, N, K, epilogue) drawn over every routing class of lsk_linear_bf16:
+    decode (M <= 16), decode slices (N or K off the block GEMM's grid),
+    the 128-row GEMM, and the block GEMM with and without a split last round."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        cls = i % 4
+        m = int(rng.integers(1, 17)) if cls == 0 else int(rng.integers(17, 3000))
+        if cls == 1:  # off the block grid: N a multiple of 32 only, or K of 32 only
+            n = 32 * int(rng.integers(1, 160))
+            k = 32 * int(rng.integers(2, 200))
+        else:
+            n = 128 * int(rng.integers(1, 80))
+            k = 128 * int(rng.integers(1, 96))
+        epi = int(rng.integers(0, 3))
+        out.append((m, n, k, epi))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k,epi", _random_shapes(24, 2026))
+def test_linear_random_shapes(gpu, m, n, k, epi):
+    """Seeded random shapes against the oracle on sampled rows (the first,
+    last, block-edge and random rows; every row when M <= 64), with the
+    auto workspace; the plan the block GEMM takes is printed with the case."""
+    layout = _lib.LAYOUT_MFMA16X32_GATEUP if epi == _lib.EPI_SILU_MUL else _lib.LAYOUT_MFMA16X32
+    w = weight(n, k, seed=m + n + k)
+    x = activations(m, k, seed=m * 7 + k)
+    r = activations(m, n, seed=m * 11 + n) if epi == _lib.EPI_RESIDUAL_ADD else None
+    print(f"case M={m} N={n} K={k} epi={epi} plan={_linear_plan(m, n, k)}", flush=True)
+    y = _gpu_linear(x, w, layout, epi, residual=r)
+    if m <= 64:
+        rows = torch.arange(m)
+    else:
+        gen = torch.Generator().manual_seed(m)
+        edges = torch.tensor([0, 1, 127, 128, 255, 256, m - 2, m - 1])
+        rows = torch.cat([edges[edges < m], torch.randint(0, m, (40,), generator=gen)]).unique()
+    yl = ref.linear(x[rows], w)
+    if epi == _lib.EPI_SILU_MUL:
+        expect = ref.silu_mul(yl, n // 2)
+    elif epi == _lib.EPI_RESIDUAL_ADD:
+        expect = r[rows] + yl
+    else:
+        expect = yl
+    assert_parity(y[rows], expect, f"M={m} N={n} K={k} epi={epi}")
+
+
 def test_lm_head_argmax_follows_torch_on_nan_and_inf(gpu):
     """Scores that are NaN, +inf or all -inf: the kernel's token is what
     torch.argmax returns on the same scores (the first NaN wins, +inf beats
