@@ -1141,7 +1141,14 @@ inline void split_plan(int T, int units, int grid, int* R, int* S) {
 // split workgroup's fp32 partial and need fewer chunks.  At 512 tokens:
 // o_proj 29.5 -> 23.9 us, QKV 32.2 -> 28.9, down_proj 45.4 -> 41.2; where
 // the blocks split fewer ways (every shape at 2048 tokens) or not at all
-// (gate_up at 512) 128-row blocks measured slower.
+// (gate_up at 512) 128-row blocks measured slower.  Also 1 when the coarser
+// plan splits two or three ways but 128-row blocks fit one round without a
+// split and the measured costs favour them: per 64-K stage at full load a
+// 128-row block takes about 0.85 us against 1.18 (192 rows) and 1.40 (256
+// rows), and a split round adds about 0.06 us per block row for its partial
+// exchange.  QKV at 768 and 1024 tokens 37.2 -> 32.6 and 41.1 -> 36.3 us,
+// o_proj at 3072 66.1 -> 61.8; down_proj at 3072 (152 stages) keeps its
+// split 256-row round.
 inline int choose_tiles(int N, int m_blocks, int grid, int units, int split_grid) {
   int a = 4;
   if (N % kRows192 != 0) {
@@ -1158,6 +1165,12 @@ inline int choose_tiles(int N, int m_blocks, int grid, int units, int split_grid
     int R = 0, S = 1;
     split_plan(T, units, split_grid, &R, &S);
     if (T < split_grid && S >= 4) return 1;
+    if (T < split_grid && S >= 2 && (N / kRows128) * m_blocks <= grid) {
+      const int stages = 2 * units;
+      const double t128 = 0.85 * stages;
+      const double tc = (a == 3 ? 1.18 : 1.40) * ((stages + S - 1) / S) + 0.06 * (a == 3 ? kRows192 : kRowsWide);
+      if (t128 < tc) return 1;
+    }
   }
   return a;
 }
