@@ -17,6 +17,7 @@ the wrong row, a dropped eps or a wrong mean fails the relative bound.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -105,6 +106,27 @@ def test_rmsnorm_linear_matches_oracle(gpu, name, m):
     y_unfused = _unfused(xn, pw, epi, residual)
     diff = (y != y_unfused).float().mean().item()
     assert diff <= 0.02, f"{name} M={m}: {diff:.4f} of the outputs differ from the unfused path"
+
+
+def _random_norm_cases(count: int, seed: int) -> list[tuple[int, int, int, int]]:
+    """(M, N, K, epilogue) with M = 1..16, N a multiple of 32 up to 8192 and K a
+    multiple of 32 up to 12288: every activation-chunk and prologue form."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 17)), 32 * int(rng.integers(1, 257)), 32 * int(rng.integers(1, 385)),
+             int(rng.integers(0, 3))) for _ in range(count)]
+
+
+@pytest.mark.parametrize("m,n,k,epi", _random_norm_cases(16, 4242))
+def test_rmsnorm_linear_random_shapes(gpu, m, n, k, epi):
+    layout = _lib.LAYOUT_MFMA16X32_GATEUP if epi == _lib.EPI_SILU_MUL else _lib.LAYOUT_MFMA16X32
+    seed = m * 131 + n + k
+    w = weight(n, k, seed=seed)
+    x = _rows(m, k, seed + 1)
+    nw = _norm_weight(k, seed + 2)
+    residual = seeded_normal((m, n), 1.0, seed + 3) if epi == _lib.EPI_RESIDUAL_ADD else None
+    pw = PackedWeight.from_rowmajor(w.to(DEV), layout)
+    y = _fused(x, nw, pw, epi, residual)
+    assert_parity(y, _expect(x, nw, w, epi, residual), f"M={m} N={n} K={k} epi={epi}")
 
 
 @pytest.mark.parametrize("name,m", [("qkv", 1), ("qkv", 16), ("gate_up", 4), ("k4096_silu", 3)])
