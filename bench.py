@@ -114,11 +114,24 @@ def measured_traffic(kernel_label: str):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (/proc/cpuinfo), or the platform's description."""
+    """The host CPU's model name, CPU family and model numbers (/proc/cpuinfo;
+    a virtual machine may report only a generic name, e.g. "AMD EPYC", whose
+    family / model then tell the generation) and whether a hypervisor runs it,
+    or the platform's description."""
     try:
+        fields = {}
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, value = line.partition(":")
+            key = key.strip()
+            if key in ("model name", "cpu family", "model", "flags") and key not in fields:
+                fields[key] = value.strip()
+        if "model name" in fields:
+            text = fields["model name"]
+            if "cpu family" in fields and "model" in fields:
+                text += f" (family {fields['cpu family']}, model {fields['model']})"
+            if "hypervisor" in fields.get("flags", "").split():
+                text += ", virtualised"
+            return text
     except OSError:
         pass
     return platform.processor() or platform.machine()
