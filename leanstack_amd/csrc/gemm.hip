@@ -1,19 +1,31 @@
-// Prefill projections (M in the hundreds to thousands) on gfx950 MFMA.
+// Projections of more than 16 rows on gfx950 MFMA:
+// y[M][N] = epilogue(x[M][K] . W[N][K]^T), W in LSK_LAYOUT_MFMA16X32 (or its
+// gate/up-interleaved form), bf16 in and out, fp32 accumulation.  Three
+// kernels; launch_gemm_linear at the end of this file picks one:
 //
-// y[M][N] = epilogue(x[M][K] . W[N][K]^T) with W in LSK_LAYOUT_MFMA16X32.
-// Because each packed 1 KB weight tile already is a v_mfma_f32_16x16x32_bf16
-// operand in lane order, the weight half of every LDS stage is a straight
-// linear copy (no swizzle, no bank conflicts on write or read).  The
-// activation half is re-tiled into the same 16x32 operand order as it is
-// copied into LDS, so both MFMA operands are read with linear 16-byte LDS
-// loads.
+//  * wdx::gemm_wdx_kernel, the prefill GEMM proper (M > 128, N a multiple of
+//    256 or 192, K of 128: every Qwen3-4B projection).  256 tokens x 256, 192
+//    or 128 weight rows x 64 K per stage and workgroup on
+//    v_mfma_f32_32x32x16_bf16: weight fragments from HBM/L2 straight into
+//    registers one stage ahead, activations DMA'd into a three-buffer LDS ring
+//    two stages ahead, a counted stage barrier, the epilogue through LDS in
+//    row order, and, with a workspace, the last partial round split along K
+//    over the idle CUs ("Split-K of the last round" below).
+//  * big::gemm256_kernel, 256 x 256 blocks with both operands staged in LDS,
+//    for the M > 128 shapes with N a multiple of 256 that the wdx kernel does
+//    not take (K an odd multiple of 64).
+//  * gemm_linear_kernel, 128 x 128 blocks for the rest of the 128-row grid
+//    (M = 17..128, or N a multiple of 128 only).  Each packed 1 KB weight
+//    tile already is a v_mfma_f32_16x16x32_bf16 operand in lane order, so the
+//    weight half of every LDS stage is a straight linear copy; the activation
+//    half is re-tiled into the same operand order as it is copied, so both
+//    operands are read with linear 16-byte LDS loads.  4 wavefronts in a 2x2
+//    arrangement, each owning 64x64 = 4x4 MFMA tiles; LDS double buffered.
 //
-// Block tile 128 (weight rows) x 128 (tokens) x 64 (K), 4 wavefronts in a 2x2
-// arrangement, each owning 64x64 = 4x4 MFMA tiles; LDS is double buffered so
-// the global loads of stage s+1 are in flight while stage s is multiplied.
-// Workgroups are remapped so that each XCD walks a contiguous run of a
+// Every kernel remaps workgroups so that each XCD walks a contiguous run of a
 // grouped (token block, weight block) order whose resident window shares its
-// weight and activation slices through the XCD's L2 (block_coords).
+// weight and activation slices through the XCD's L2.  Rows of M <= 16 and
+// shapes off the 128-row grid go to the decode kernels (decode.hip).
 //
 // Reference arithmetic replaced: F.linear at
 // src/leanstack/runtime/qwen_explicit.py:748, :819, :828, :830, :1202-1208 and
