@@ -469,8 +469,8 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 
 }  // namespace big
 
-// Weights-direct variant of the 256x256x64 kernel (and of a 192x256x64 one,
-// chosen by choose_tiles).  Each wave loads its own weight fragments from
+// Weights-direct variant of the 256x256x64 kernel (and of 192x256x64 and
+// 128x256x64 ones, chosen by choose_tiles).  Each wave loads its own weight fragments from
 // global memory straight into registers: a packed 1 KB tile already is MFMA
 // operand data in lane order, so a 32-row A fragment is two 512-byte
 // contiguous runs and needs no LDS staging.  Only the activations go
@@ -478,9 +478,10 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 // no ds_write instructions.  With 256-row blocks each wave owns 64 weight
 // rows over all 256 tokens, so every weight line is fetched once per
 // workgroup (32 KB of weights, 32 KB of activations per stage and CU through
-// the texture path, 128 KB of LDS fragment reads); the 192-row blocks keep
-// two waves across N and two across tokens, and there the two waves that
-// share a weight-row half fetch the same lines, the second mostly from L1.
+// the texture path, 128 KB of LDS fragment reads), and with 128-row blocks
+// 32; the 192-row blocks keep two waves across N and two across tokens, and
+// there the two waves that share a weight-row half fetch the same lines, the
+// second mostly from L1.
 // Weight fragments are prefetched one stage ahead into the idle one of two
 // register sets, activations two stages ahead into the free one of three
 // LDS buffers; the stage loop is unrolled by six so both rotations run
@@ -492,7 +493,8 @@ constexpr int BN = 256, BM = 256, BK = 64;
 // workgroup are TB/2 across N and 8/TB across the 256 tokens, so a block
 // has 16*A*TB weight rows.  Built: (A, TB) = (2, 8) -> 256 rows, every wave
 // over all tokens; (3, 4) -> 192 rows (QKV at 2048 tokens: 256 blocks in
-// one round instead of 192 blocks of 256 rows).
+// one round instead of 192 blocks of 256 rows); (1, 8) -> 128 rows, every
+// wave over all tokens (small token counts, see choose_tiles).
 template <int A, int TB>
 constexpr int kBN = 16 * A * TB;
 constexpr int kRowsWide = kBN<2, 8>;  // 256
