@@ -478,8 +478,8 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
 // no ds_write instructions.  With 256-row blocks each wave owns 64 weight
 // rows over all 256 tokens, so every weight line is fetched once per
 // workgroup (32 KB of weights, 32 KB of activations per stage and CU through
-// the texture path, 128 KB of LDS fragment reads), and with 128-row blocks
-// 32; the 192-row blocks keep two waves across N and two across tokens, and
+// the texture path, 128 KB of LDS fragment reads), with 128-row blocks 32
+// rows the same way; the 192-row blocks keep two waves across N and two across tokens, and
 // there the two waves that share a weight-row half fetch the same lines, the
 // second mostly from L1.
 // Weight fragments are prefetched one stage ahead into the idle one of two
