@@ -108,7 +108,9 @@ int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* 
  * plan[2] = blocks whose K range is split over several workgroups, plan[3] =
  * workgroups (K chunks) per split block (1: no split).  plan = {0, 0, 0, 1}
  * when the call takes the decode kernels (M <= 16, or a shape off the block
- * GEMM's tile grid) or the plain 128-row GEMM.  For tests and tuning; no
+ * GEMM's tile grid) or the plain 128-row GEMM.  A workspace smaller than
+ * lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K) is refused with
+ * LSK_ERR_WORKSPACE, as lsk_linear_bf16 refuses it.  For tests and tuning; no
  * counterpart in the reference, whose F.linear hides its cuBLAS plan. */
 int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int plan[4]);
 

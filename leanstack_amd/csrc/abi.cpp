@@ -80,7 +80,18 @@ int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int* plan) {
   // The routing of lsk_linear_bf16: decode kernels up to kDecodeMaxM rows and
   // off the GEMM tile grid, the block GEMM otherwise.
   if (M <= lsk::kDecodeMaxM || N % lsk::kGemmBN != 0 || K % lsk::kGemmBK != 0) return LSK_OK;
-  const hipError_t err = lsk::plan_gemm_linear(M, N, K, ws_bytes, plan);
+  hipError_t err;
+  if (ws_bytes > 0) {
+    // The workspace lsk_linear_bf16 would refuse is refused here too.
+    int device = 0;
+    err = hipGetDevice(&device);
+    if (err != hipSuccess) return hip_fail(err, "hipGetDevice");
+    const size_t need = lsk::gemm_workspace_bytes(device, M, N, K, &err);
+    if (err != hipSuccess) return hip_fail(err, "prefill workspace size");
+    if (ws_bytes < need)
+      return fail(LSK_ERR_WORKSPACE, "prefill workspace needs %zu bytes (got %zu)", need, ws_bytes);
+  }
+  err = lsk::plan_gemm_linear(M, N, K, ws_bytes, plan);
   if (err != hipSuccess) return hip_fail(err, "prefill plan");
   return LSK_OK;
 }

@@ -1266,21 +1266,17 @@ size_t gemm_workspace_bytes(int device, int M, int N, int K, hipError_t* status)
 }
 
 // The block GEMM's plan on the current device: `grid` = the CUs the last,
-// partial round may split over (0 without a workspace; with one, every CU
-// the workspace has partial slots for) and the block height as choose_tiles
-// returns it.  Shared by the launch and lsk_linear_plan.
-static hipError_t wdx_plan(int M, int N, int K, bool has_ws, size_t ws_bytes, int* grid_out, int* tiles_out) {
+// partial round may split over (0 without a workspace, else every CU: both
+// callers have checked that a workspace holds gemm_workspace_bytes) and the
+// block height as choose_tiles returns it.  Shared by the launch and
+// lsk_linear_plan.
+static hipError_t wdx_plan(int M, int N, int K, bool has_ws, int* grid_out, int* tiles_out) {
   int device = 0, cus = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return err;
   err = sk_grid(device, &cus);
   if (err != hipSuccess) return err;
-  int grid = 0;
-  if (has_ws && ws_bytes > kSkPartialsOffset) {
-    grid = cus;
-    const size_t fit = (ws_bytes - kSkPartialsOffset) / kSkPartialBytes;
-    if ((size_t)grid > fit) grid = (int)fit;
-  }
+  const int grid = has_ws ? cus : 0;
   *grid_out = grid;
   *tiles_out = wdx::choose_tiles(N, (M + wdx::BM - 1) / wdx::BM, cus, K / kTileK / 4, grid);
   return hipSuccess;
@@ -1293,7 +1289,7 @@ hipError_t plan_gemm_linear(int M, int N, int K, size_t ws_bytes, int plan[4]) {
   plan[3] = 1;
   if (!sk_shape(M, N, K)) return hipSuccess;
   int grid = 0, tiles = 0;
-  const hipError_t err = wdx_plan(M, N, K, ws_bytes > 0, ws_bytes, &grid, &tiles);
+  const hipError_t err = wdx_plan(M, N, K, ws_bytes > 0, &grid, &tiles);
   if (err != hipSuccess) return err;
   const int rows = tiles == 3 ? wdx::kRows192 : tiles == 1 ? wdx::kRows128 : wdx::kRowsWide;
   const int T = (N / rows) * ((M + wdx::BM - 1) / wdx::BM);
@@ -1313,7 +1309,7 @@ hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M,
     // With a workspace, the partial last round is split over every CU (as
     // many as the workspace has partial slots for).
     int grid = 0, tiles = 0;
-    const hipError_t err = wdx_plan(M, N, K, workspace != nullptr, ws_bytes, &grid, &tiles);
+    const hipError_t err = wdx_plan(M, N, K, workspace != nullptr, &grid, &tiles);
     if (err != hipSuccess) return err;
     void* ws = grid > 0 ? workspace : nullptr;
     auto go = [&](auto a_tag, auto tb_tag) -> hipError_t {

@@ -174,15 +174,16 @@ size_t gemm_workspace_bytes(int device, int M, int N, int K, hipError_t* status)
 void set_linear_wait_limit(unsigned polls);
 
 // Prefill GEMM launch (any M >= 1; used for M > kDecodeMaxM).  With a
-// workspace of at least gemm_workspace_bytes() the last partial round of
-// output blocks is split along K over the idle CUs;
+// workspace (the caller has checked it holds gemm_workspace_bytes()) the
+// last partial round of output blocks is split along K over the idle CUs;
 // with none, one workgroup per output block.
-// The prefill GEMM's plan for M rows of an [N, K] weight with ws_bytes of
-// workspace on the current device: {block rows, blocks, split blocks,
-// chunks per split block}; {0, 0, 0, 1} when the shape takes another kernel.
-hipError_t plan_gemm_linear(int M, int N, int K, size_t ws_bytes, int plan[4]);
 hipError_t launch_gemm_linear(const void* w, int N, int K, const void* x, int M, int ldx,
                               void* y, int ldy, Epilogue epi, const void* residual, int ldr,
                               void* workspace, size_t ws_bytes, hipStream_t stream);
+// The prefill GEMM's plan for M rows of an [N, K] weight on the current
+// device, with a workspace (ws_bytes > 0, checked as for the launch) or
+// without: {block rows, blocks, split blocks, chunks per split block};
+// {0, 0, 0, 1} when the shape takes another kernel.
+hipError_t plan_gemm_linear(int M, int N, int K, size_t ws_bytes, int plan[4]);
 
 }  // namespace lsk

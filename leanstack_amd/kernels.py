@@ -22,6 +22,17 @@ def _require_device(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what} must be a GPU tensor, got device {t.device}")
 
 
+def _one_device(first: torch.Tensor, *named: tuple[torch.Tensor | None, str]) -> torch.device:
+    """The device of `first`, after checking that every other tensor given
+    (None skipped) lives on it: the C layer launches on one device and sees
+    only pointers."""
+    dev = first.device
+    for t, what in named:
+        if t is not None and t.device != dev:
+            raise ValueError(f"{what} is on {t.device}, the call's tensors are on {dev}")
+    return dev
+
+
 def _rows(x: torch.Tensor, k: int, what: str) -> tuple[torch.Tensor, int, int]:
     """View x as [M, k] rows with unit column stride; returns (x2d, M, ld)."""
     if x.dtype != torch.bfloat16:
@@ -139,13 +150,15 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
     if workspace is not None:
         _require_device(workspace, "workspace")
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
-    status = lib.lsk_linear_bf16(
-        weight.data.data_ptr(), weight.layout, weight.n, weight.k,
-        x2.data_ptr(), m, ldx,
-        out.data_ptr(), n_out,
-        epilogue, res_ptr, ldr,
-        ws_ptr, ws_bytes, stream_handle(),
-    )
+    dev = _one_device(x, (weight.data, "weight"), (out, "out"), (r2, "residual"), (workspace, "workspace"))
+    with torch.cuda.device(dev):
+        status = lib.lsk_linear_bf16(
+            weight.data.data_ptr(), weight.layout, weight.n, weight.k,
+            x2.data_ptr(), m, ldx,
+            out.data_ptr(), n_out,
+            epilogue, res_ptr, ldr,
+            ws_ptr, ws_bytes, stream_handle(),
+        )
     _lib.check(status, "lsk_linear_bf16")
     return out
 
@@ -182,13 +195,15 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weigh
     res_ptr, ldr = (None, 0) if r2 is None else (r2.data_ptr(), ldr)
     if r2 is not None:
         _require_device(r2, "residual")
-    status = lib.lsk_rmsnorm_linear_bf16(
-        weight.data.data_ptr(), weight.layout, weight.n, weight.k,
-        x2.data_ptr(), m, ldx,
-        nw.data_ptr(), float(eps),
-        out.data_ptr(), n_out,
-        epilogue, res_ptr, ldr, stream_handle(),
-    )
+    dev = _one_device(x, (weight.data, "weight"), (nw, "norm_weight"), (out, "out"), (r2, "residual"))
+    with torch.cuda.device(dev):
+        status = lib.lsk_rmsnorm_linear_bf16(
+            weight.data.data_ptr(), weight.layout, weight.n, weight.k,
+            x2.data_ptr(), m, ldx,
+            nw.data_ptr(), float(eps),
+            out.data_ptr(), n_out,
+            epilogue, res_ptr, ldr, stream_handle(),
+        )
     _lib.check(status, "lsk_rmsnorm_linear_bf16")
     return out
 
@@ -259,16 +274,19 @@ def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
             raise ValueError(f"workspace must be 'auto' or a tensor, not {workspace!r}")
         workspace = attention_workspace(qkv.device, n_q, n_kv, d, s_max)
     _require_device(workspace, "workspace")
+    dev = _one_device(qkv, (q_norm_weight, "q_norm_weight"), (k_norm_weight, "k_norm_weight"), (cos, "cos"),
+                      (sin, "sin"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out"),
+                      (workspace, "workspace"), (pos if on_device else None, "pos"))
     common = (flat[0].data_ptr(), n_q, n_kv, d, flat[1].data_ptr(), flat[2].data_ptr(), float(eps),
               flat[3].data_ptr(), flat[4].data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), s_max)
-    tail = (float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-            stream_handle())
-    if on_device:
-        status = lib.lsk_decode_attention_at_bf16(*common, pos.data_ptr(), *tail)
-        _lib.check(status, "lsk_decode_attention_at_bf16")
-    else:
-        status = lib.lsk_decode_attention_bf16(*common, int(pos), *tail)
-        _lib.check(status, "lsk_decode_attention_bf16")
+    tail = (float(scale), out.data_ptr(), workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    with torch.cuda.device(dev):
+        tail += (stream_handle(),)
+        if on_device:
+            status = lib.lsk_decode_attention_at_bf16(*common, pos.data_ptr(), *tail)
+        else:
+            status = lib.lsk_decode_attention_bf16(*common, int(pos), *tail)
+    _lib.check(status, "lsk_decode_attention_at_bf16" if on_device else "lsk_decode_attention_bf16")
     return out
 
 
@@ -317,23 +335,27 @@ def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: i
     if logits_out is not None:
         _require_device(logits_out, "logits_out")
         logits_ptr = logits_out.data_ptr()
+    dev = _one_device(hidden, (weight.data, "weight"), (out, "out"), (logits_out, "logits_out"),
+                      (norm_weight, "norm_weight"), (workspace.buffer, "workspace"))
     if norm_weight is not None:
         _require_device(norm_weight, "norm_weight")
         nw = norm_weight.reshape(-1).contiguous()
-        status = lib.lsk_rmsnorm_lm_head_argmax_bf16(
-            weight.data.data_ptr(), weight.layout, v, weight.k, h2.data_ptr(), m, ldx, nw.data_ptr(), float(eps),
-            logits_ptr, logits_mode, out.data_ptr(), workspace.buffer.data_ptr(), workspace.buffer.numel(),
-            stream_handle(),
-        )
+        with torch.cuda.device(dev):
+            status = lib.lsk_rmsnorm_lm_head_argmax_bf16(
+                weight.data.data_ptr(), weight.layout, v, weight.k, h2.data_ptr(), m, ldx, nw.data_ptr(), float(eps),
+                logits_ptr, logits_mode, out.data_ptr(), workspace.buffer.data_ptr(), workspace.buffer.numel(),
+                stream_handle(),
+            )
         _lib.check(status, "lsk_rmsnorm_lm_head_argmax_bf16")
         return out
-    status = lib.lsk_lm_head_argmax_bf16(
-        weight.data.data_ptr(), weight.layout, v, weight.k,
-        h2.data_ptr(), m, ldx,
-        logits_ptr, logits_mode,
-        out.data_ptr(),
-        workspace.buffer.data_ptr(), workspace.buffer.numel(), stream_handle(),
-    )
+    with torch.cuda.device(dev):
+        status = lib.lsk_lm_head_argmax_bf16(
+            weight.data.data_ptr(), weight.layout, v, weight.k,
+            h2.data_ptr(), m, ldx,
+            logits_ptr, logits_mode,
+            out.data_ptr(),
+            workspace.buffer.data_ptr(), workspace.buffer.numel(), stream_handle(),
+        )
     _lib.check(status, "lsk_lm_head_argmax_bf16")
     return out
 
@@ -358,9 +380,11 @@ def lm_head_argmax_noalloc(hidden: torch.Tensor, weight: PackedWeight, out: torc
         raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{weight.n}")
     for t, what in ((hidden, "hidden"), (weight.data, "weight"), (out, "out")):
         _require_device(t, what)
-    status = _lib.load().lsk_lm_head_argmax_noalloc_bf16(
-        weight.data.data_ptr(), weight.layout, weight.n, weight.k, hidden.data_ptr(), m, weight.k,
-        logits_out.data_ptr() if logits_out is not None else None, logits_mode, out.data_ptr(), stream_handle())
+    dev = _one_device(hidden, (weight.data, "weight"), (out, "out"), (logits_out, "logits_out"))
+    with torch.cuda.device(dev):
+        status = _lib.load().lsk_lm_head_argmax_noalloc_bf16(
+            weight.data.data_ptr(), weight.layout, weight.n, weight.k, hidden.data_ptr(), m, weight.k,
+            logits_out.data_ptr() if logits_out is not None else None, logits_mode, out.data_ptr(), stream_handle())
     _lib.check(status, "lsk_lm_head_argmax_noalloc_bf16")
     return out
 
@@ -371,13 +395,27 @@ class StackStep:
 
     `projections` is a list of dicts with keys x, weight (PackedWeight), out,
     and optionally epilogue, residual, depends_on (index of an earlier entry:
-    every entry up to it finishes before this one reads its inputs)."""
+    every entry up to it finishes before this one reads its inputs).  The
+    program holds the tensors' addresses, so x, out and residual are used in
+    place (rows of unit column stride, row strides a multiple of 8 elements,
+    16-byte aligned): one entry's out can be a later entry's x.  A tensor
+    that would need a copy is refused."""
 
     def __init__(self, projections: list[dict], m: int, device: torch.device | str) -> None:
         lib = _lib.load()
+        device = torch.device(device)
         count = len(projections)
         arr = (_lib.Projection * count)()
         self._keep = []  # tensors whose pointers the program holds
+
+        def in_place(t: torch.Tensor, t2: torch.Tensor, what: str) -> None:
+            if t2.data_ptr() != t.data_ptr() or t2.stride(-1) != 1:
+                raise ValueError(f"{what} must be usable in place (unit column stride, row stride a multiple "
+                                 f"of 8, 16-byte aligned): the program holds its address")
+            if t.device.type != "cuda" or t.device.index != (device.index if device.index is not None
+                                                             else torch.cuda.current_device()):
+                raise ValueError(f"{what} is on {t.device}, the program on {device}")
+
         for i, spec in enumerate(projections):
             w = spec["weight"]
             if not isinstance(w, PackedWeight):
@@ -387,15 +425,21 @@ class StackStep:
             x2, xm, ldx = _rows(x, w.k, f"projection {i} x")
             if xm != m:
                 raise ValueError(f"projection {i}: x has {xm} rows, the step runs M={m}")
+            in_place(x, x2, f"projection {i} x")
+            in_place(w.data, w.data, f"projection {i} weight")
             n_out = w.n // 2 if epi == _lib.EPI_SILU_MUL else w.n
-            if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or out.reshape(-1, n_out).shape[0] != m:
+            if out.dtype != torch.bfloat16 or out.shape[-1] != n_out or out.numel() != m * n_out:
                 raise ValueError(f"projection {i}: out must be bfloat16 [{m}, {n_out}]")
             o2 = out.reshape(-1, n_out)
+            in_place(out, o2, f"projection {i} out")
             ldy = o2.stride(0) if m > 1 else n_out
             res = spec.get("residual")
             res_ptr, ldr = None, 0
             if res is not None:
                 r2, rm, ldr = _rows(res, w.n, f"projection {i} residual")
+                if rm != m:
+                    raise ValueError(f"projection {i}: residual has {rm} rows, the step runs M={m}")
+                in_place(res, r2, f"projection {i} residual")
                 res_ptr = r2.data_ptr()
                 self._keep.append(r2)
             self._keep += [x2, o2, w.data]
@@ -403,15 +447,18 @@ class StackStep:
                                      epi, res_ptr, ldr, int(spec.get("depends_on", -1)))
         self.count = count
         self.m = m
-        self.program = torch.empty(lib.lsk_stack_program_bytes(count), dtype=torch.uint8, device=device)
-        self.workspace = torch.zeros(lib.lsk_stack_workspace_bytes(count), dtype=torch.uint8, device=device)
-        _lib.check(lib.lsk_stack_prepare(arr, count, m, self.program.data_ptr(), self.program.numel()),
-                   "lsk_stack_prepare")
+        with torch.cuda.device(device):
+            self.program = torch.empty(lib.lsk_stack_program_bytes(count), dtype=torch.uint8, device=device)
+            self.workspace = torch.zeros(lib.lsk_stack_workspace_bytes(count), dtype=torch.uint8, device=device)
+            status = lib.lsk_stack_prepare(arr, count, m, self.program.data_ptr(), self.program.numel())
+        _lib.check(status, "lsk_stack_prepare")
 
     def launch(self) -> None:
         lib = _lib.load()
-        _lib.check(lib.lsk_stack_run(self.program.data_ptr(), self.count, self.workspace.data_ptr(),
-                                     self.workspace.numel(), stream_handle()), "lsk_stack_run")
+        with torch.cuda.device(self.program.device):
+            status = lib.lsk_stack_run(self.program.data_ptr(), self.count, self.workspace.data_ptr(),
+                                       self.workspace.numel(), stream_handle())
+        _lib.check(status, "lsk_stack_run")
 
     def error(self) -> int:
         """Read and clear the error word (synchronises): 0 if every wait completed."""

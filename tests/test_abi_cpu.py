@@ -252,6 +252,18 @@ def test_wrappers_refuse_outputs_of_the_wrong_size():
         kernels.lm_head_argmax(x, w, out=torch.empty(8, dtype=torch.long))
 
 
+def test_wrappers_refuse_tensors_on_another_device():
+    """Every tensor of a call must live on the first one's device: the C layer
+    launches on one device and would take another device's pointers as its
+    own.  (Meta tensors stand in for a second device here.)"""
+    from leanstack_amd import kernels
+
+    a = torch.zeros(4)
+    assert kernels._one_device(a, (torch.zeros(2), "w"), (None, "residual")) == a.device
+    with pytest.raises(ValueError, match="residual is on meta"):
+        kernels._one_device(a, (torch.zeros(2), "w"), (torch.zeros(2, device="meta"), "residual"))
+
+
 def test_launch_next_refuses_a_bad_token_buffer():
     """DecodeStep.launch_next's token buffer: 1-D int64 on the step's device."""
     from leanstack_amd.stack import DecodeStep

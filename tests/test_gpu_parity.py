@@ -403,6 +403,13 @@ def test_split_k_workspace_contract(gpu):
     assert kernels.linear_error(ws) == 0
     with pytest.raises(ValueError):
         kernels.linear(x.to(dev), pw, workspace=ws[: nbytes // 2])
+    # The plan refuses the workspace the launch refuses, and plans the split
+    # round only with a whole one.
+    lib = _lib.load()
+    plan = (ctypes.c_int * 4)(9, 9, 9, 9)
+    assert lib.lsk_linear_plan(m, n, k, nbytes - 1, plan) == _lib.ERR_WORKSPACE
+    assert lib.lsk_linear_plan(m, n, k, nbytes, plan) == _lib.OK and plan[2] > 0 and plan[3] > 1
+    assert lib.lsk_linear_plan(m, n, k, 0, plan) == _lib.OK and plan[2] == 0 and plan[3] == 1
 
 
 def _prefill_case(name, m, seed):

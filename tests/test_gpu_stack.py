@@ -176,6 +176,19 @@ def test_stack_rejects_bad_programs(gpu):
     with pytest.raises(ValueError):
         kernels.StackStep([{"x": torch.zeros((1, 128), device=DEV, dtype=torch.bfloat16), "weight": small,
                             "out": torch.empty((1, 64), device=DEV, dtype=torch.bfloat16)}], 1, DEV)
+    # Tensors the program could only use through a copy: the program holds
+    # addresses, so a copy would cut a producer -> consumer chain silently.
+    wide = torch.zeros((2, G.hidden_size + 1), device=DEV, dtype=torch.bfloat16)
+    y2 = torch.empty((2, G.qkv_dim), device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="in place"):  # row stride not a multiple of 8
+        kernels.StackStep([{"x": wide[:, : G.hidden_size], "weight": w["qkv"], "out": y2}], 2, DEV)
+    with pytest.raises(ValueError, match="in place"):  # output columns not contiguous
+        kernels.StackStep([{"x": torch.zeros((2, G.hidden_size), device=DEV, dtype=torch.bfloat16),
+                            "weight": w["qkv"],
+                            "out": torch.empty((G.qkv_dim, 2), device=DEV, dtype=torch.bfloat16).t()}], 2, DEV)
+    with pytest.raises(ValueError):  # out of the wrong size
+        kernels.StackStep([{"x": x, "weight": w["qkv"], "out": torch.empty((2, G.qkv_dim), device=DEV,
+                                                                        dtype=torch.bfloat16)}], 1, DEV)
 
 
 def test_stack_reused_buffer_across_layers(gpu):
