@@ -340,9 +340,14 @@ class _RegionReader:
                 got = f.readinto(memoryview(self.stage[slot].numpy())[:n])
                 if got != n:
                     raise ValueError(f"{path}: {done + got} of {nbytes} bytes at offset {file_offset} (truncated file)")
-                self.dst[arena_offset + done : arena_offset + done + n].copy_(self.stage[slot][:n], non_blocking=True)
+                # The copy and its event on the arena device's stream, so the
+                # event covers the copy whichever device is current.
+                stream = torch.cuda.current_stream(self.dst.device)
+                with torch.cuda.stream(stream):
+                    self.dst[arena_offset + done : arena_offset + done + n].copy_(self.stage[slot][:n],
+                                                                                  non_blocking=True)
                 ev = torch.cuda.Event()
-                ev.record()
+                ev.record(stream)
                 self.done[slot] = ev
                 done += n
                 i += 1

@@ -231,3 +231,29 @@ def test_real_shape_layer_from_pack_runs_the_dispatch_path(gpu, tmp_path):
     tok = dispatch.select_semantic_greedy_token(runtime, h.view(1, 1, -1).cuda())
     normed = ref.rmsnorm(h.view(1, -1), ckpt["model.norm.weight"], g.rms_norm_eps).view(-1)
     assert tok.item() == ref.logits_argmax(normed, ckpt["model.embed_tokens.weight"]).item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_device_arena_matches_host_arena_through_small_chunks(gpu, tiny_pack, monkeypatch, per_tensor):
+    """The device loader stages file regions through two pinned buffers,
+    reading one while the other is copied; with 4 KB chunks every region takes
+    many turns of both.  The device arena's weight bytes equal the host
+    arena's, read straight from the files (whole-file images, or one tensor at
+    a time with another alignment)."""
+    from leanstack_amd import leanserve
+    from leanstack_amd.leanserve import ResidentArena, build_resident_buffer_plan, load_pack_into_arena
+    from leanstack_amd.pack import geometry_from_manifest
+
+    _, out, manifest = tiny_pack
+    monkeypatch.setattr(leanserve, "LOAD_CHUNK_BYTES", 4096)
+    extra = {"alignment": 8192} if per_tensor else {}
+    plan = build_resident_buffer_plan(geometry_from_manifest(manifest), buckets=(), **extra)
+    host, dev = ResidentArena(plan, "cpu"), ResidentArena(plan, "cuda:0")
+    s_host = load_pack_into_arena(out, manifest, host)
+    s_dev = load_pack_into_arena(out, manifest, dev)
+    assert s_host == s_dev and (s_dev["per_tensor"] > 0) == per_tensor
+    got = dev.buffer.cpu()
+    for e in plan.entries:
+        if e.name in host.weight_names():
+            assert torch.equal(got[e.offset : e.end], host.buffer[e.offset : e.end]), e.name
