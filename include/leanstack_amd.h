@@ -118,7 +118,7 @@ int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int plan[4]);
  *   w_packed   device, layout LSK_LAYOUT_MFMA16X32 (epilogue NONE / RESIDUAL_ADD)
  *              or LSK_LAYOUT_MFMA16X32_GATEUP (epilogue SILU_MUL; N = 2*I)
  *   x          device bf16, row m at x + m*ldx (ldx >= K, ldx % 8 == 0,
- *              ldx <= 2^22, 16-byte aligned)
+ *              ldx <= 2^22 - 8, 16-byte aligned)
  *   y          device bf16, row m at y + m*ldy; N columns, or N/2 for
  *              SILU_MUL (ldy % 4 == 0, 8-byte aligned)
  *   residual   device bf16 [M][N] at stride ldr, RESIDUAL_ADD only (else NULL)

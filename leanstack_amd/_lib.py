@@ -38,6 +38,8 @@ ERR_WORKSPACE = -4
 
 # Largest M served by the decode/verify kernel (kDecodeMaxM in the library).
 DECODE_MAX_M = 16
+# Largest activation row stride in elements (kMaxActivationStride).
+MAX_ACTIVATION_STRIDE = (1 << 22) - 8
 
 _c_int = ctypes.c_int
 _c_size = ctypes.c_size_t

@@ -620,7 +620,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][TB], const Args& g, 
   const int KT = g.KT;
   const int rmax = min(g.M - m0, BM) - 1;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(g.x + (size_t)m0 * g.ldx), (short)0, (rmax + 1) * g.ldx * 2, 0x00020000);
+      (void*)(g.x + (size_t)m0 * g.ldx), (short)0, (int)((unsigned)(rmax + 1) * (unsigned)g.ldx * 2u), 0x00020000);
 
   // This lane's element of weight fragment (a=0, q=0) at stage 0.
   const bf16x8_t* wl =

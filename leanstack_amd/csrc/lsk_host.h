@@ -23,8 +23,9 @@ constexpr int kDecodeMaxM = 16;
 
 // Largest activation row stride (elements) of a projection: the prefill
 // kernel reads a 256-row block of x through a buffer descriptor whose byte
-// offsets are 32-bit, so 256 * ldx * 2 must stay below 2^31.
-constexpr int kMaxActivationStride = 1 << 22;
+// offsets are 32-bit, so 256 * ldx * 2 must stay below 2^31 (and ldx is a
+// multiple of 8).
+constexpr int kMaxActivationStride = (1 << 22) - 8;
 
 // Decode attention geometry (attention.hip): the rows attended are split into
 // at most kAttnMaxChunks chunks of a multiple of kAttnMinChunkRows rows.

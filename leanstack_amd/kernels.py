@@ -34,13 +34,16 @@ def _one_device(first: torch.Tensor, *named: tuple[torch.Tensor | None, str]) ->
 
 
 def _rows(x: torch.Tensor, k: int, what: str) -> tuple[torch.Tensor, int, int]:
-    """View x as [M, k] rows with unit column stride; returns (x2d, M, ld)."""
+    """View x as [M, k] rows with unit column stride; returns (x2d, M, ld).
+    Rows the kernels cannot read in place (column stride, row stride not a
+    multiple of 8 or above the library's largest, misalignment) are copied."""
     if x.dtype != torch.bfloat16:
         raise ValueError(f"{what} must be bfloat16, got {x.dtype}")
     if x.shape[-1] != k:
         raise ValueError(f"{what} last dim {x.shape[-1]} != K={k}")
     x2 = x.reshape(-1, k)
-    if x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) % 8) or x2.data_ptr() % 16:
+    if (x2.stride(-1) != 1 or (x2.shape[0] > 1 and (x2.stride(0) % 8 or x2.stride(0) > _lib.MAX_ACTIVATION_STRIDE))
+            or x2.data_ptr() % 16):
         x2 = x2.contiguous()
     ld = x2.stride(0) if x2.shape[0] > 1 else k
     return x2, x2.shape[0], ld

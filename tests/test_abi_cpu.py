@@ -44,7 +44,7 @@ FAKE = 0x10000  # a 64 KiB-aligned non-null address: never dereferenced, calls f
     (dict(m=0), _lib.ERR_INVALID),
     (dict(ldx=2552), _lib.ERR_INVALID),      # ldx < K
     (dict(ldx=2564), _lib.ERR_INVALID),      # ldx not a multiple of 8
-    (dict(ldx=(1 << 22) + 8), _lib.ERR_INVALID),  # beyond the 32-bit activation offsets
+    (dict(ldx=1 << 22), _lib.ERR_INVALID),   # 256 rows x ldx x 2 bytes would reach 2^31
     (dict(epi=1), _lib.ERR_INVALID),         # SiLU needs the gate_up layout
     (dict(epi=5), _lib.ERR_INVALID),
     (dict(epi=2), _lib.ERR_INVALID),         # residual-add without a residual

@@ -332,6 +332,34 @@ def test_strided_activations(gpu):
     assert_parity(y, ref.linear(x, w), "strided x")
 
 
+@pytest.mark.parametrize("m", [5, 300])
+def test_largest_activation_stride(gpu, m):
+    """x rows at the largest stride the ABI accepts, 2^22 - 8 elements: a
+    256-row block of them spans 2^31 - 4096 bytes, the prefill kernel's
+    32-bit activation descriptor at its limit (M = 300: two token blocks,
+    the second part-full; M = 5: the decode kernel).  One step wider, the
+    ABI refuses the stride and the wrapper reads the rows through a copy."""
+    n, k = 2560, 4096
+    ld = _lib.MAX_ACTIVATION_STRIDE
+    assert ld == (1 << 22) - 8
+    w = weight(n, k, seed=91)
+    x = activations(m, k, seed=910 + m)
+    expect = ref.linear(x, w)
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(w.to(dev))
+    for stride in (ld, ld + 8):
+        wide = torch.empty((m, stride), device=dev, dtype=torch.bfloat16)
+        wide[:, :k] = x.to(dev)
+        y = kernels.linear(wide[:, :k], pw)
+        if stride > ld:
+            status = _lib.load().lsk_linear_bf16(pw.data.data_ptr(), pw.layout, n, k, wide.data_ptr(), m, stride,
+                                                 y.data_ptr(), n, 0, None, 0, None, 0, None)
+            assert status == _lib.ERR_INVALID, _lib.last_error()
+        torch.cuda.synchronize()
+        del wide
+        assert_parity(y.cpu(), expect, f"x at stride {stride}, M={m}")
+
+
 def test_rejects_bad_shapes_before_launch(gpu):
     dev = torch.device("cuda:0")
     pw = PackedWeight.from_rowmajor(weight(64, 64, seed=1).to(dev))
