@@ -52,11 +52,12 @@ def test_o_proj_gemv_config1(gpu):
 
 
 @pytest.mark.parametrize("name", sorted(PROJ))
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
 def test_decode_projection(gpu, name, m):
     """Every M of the decode forms: the staged-activation kernels switch their
     chunks per lane with M (QKV 1..5 up to M = 8, o_proj 1..6 up to M = 6,
-    down 2..4 up to M = 3), then fragment loads per tile."""
+    down 2..4 up to M = 3), then fragment loads per tile; M = 9..15 leave
+    part of the 16 MFMA columns unused."""
     n, k = PROJ[name]
     w = weight(n, k, seed=10 + m)
     x = activations(m, k, seed=100 + m)
@@ -65,7 +66,7 @@ def test_decode_projection(gpu, name, m):
     assert_parity(y, expect, f"{name} M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
 def test_decode_gate_up_silu(gpu, m):
     """Every M of the gate_up decode forms (4 waves x 10 pairs up to M = 2,
     then 8 x 5 with 1..5 staged chunks per lane, and the 16-row kernel)."""
@@ -77,7 +78,7 @@ def test_decode_gate_up_silu(gpu, m):
     assert_parity(y, expect, f"gate_up+silu M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 12])
 def test_decode_down_residual(gpu, m):
     n, k = G.hidden_size, G.intermediate_size
     w = weight(n, k, seed=30 + m)
@@ -87,7 +88,7 @@ def test_decode_down_residual(gpu, m):
     assert_parity(y, r + ref.linear(x, w), f"down+residual M={m}")
 
 
-@pytest.mark.parametrize("m", [1, 5, 6])
+@pytest.mark.parametrize("m", [1, 5, 6, 12])
 def test_decode_o_residual(gpu, m):
     """o_proj with the residual epilogue (values read before the weight stream)."""
     n, k = G.hidden_size, G.q_dim
