@@ -67,8 +67,7 @@ def _device_index(device: torch.device) -> int:
 
 def _device_workspace(cache: dict[int, torch.Tensor], device: torch.device, nbytes: int, what: str) -> torch.Tensor:
     """The zero-filled workspace of `cache` for `device`, grown to `nbytes`.
-    One per device: calls that share it must be stream-ordered (callers on
-    concurrent streams pass workspaces of their own).  It is never allocated
+    One per device: calls that share it must be stream-ordered.  It is never allocated
     while the stream is being captured, so a captured graph never replays a
     workspace's allocation or zero fill."""
     key = _device_index(device)
@@ -120,11 +119,13 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
     epilogue EPI_NONE (N' = N), EPI_SILU_MUL (gate_up layout, N' = N/2,
     SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection).
     workspace: "auto" uses the device's split-K workspace for prefill shapes
-    (prefill_workspace; calls on concurrent streams pass their own), None
-    runs one workgroup per output block, a uint8 device tensor is used as
-    given.  A split-K workgroup whose bounded wait gives up (possible only
-    when another kernel holds CUs the split needs) sets the workspace's error
-    word (linear_error) and writes NaN to its tiles."""
+    (prefill_workspace; for calls ordered on one stream), None runs one
+    workgroup per output block with no waits (the form for prefill calls
+    that may run concurrently with other kernels on the device), a uint8
+    device tensor is used as given.  A split-K workgroup whose bounded wait
+    gives up (possible only when another kernel holds CUs the split needs)
+    sets the workspace's error word (linear_error) and writes NaN to its
+    tiles."""
     if not isinstance(weight, PackedWeight):
         raise ValueError("weight must be a PackedWeight (pack it with leanstack_amd.layout / leanserve)")
     lib = _lib.load()
