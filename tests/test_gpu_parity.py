@@ -246,9 +246,10 @@ def test_prefill_residual(gpu):
     assert_parity(y, r + ref.linear(x, w), "o_proj+residual prefill")
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
 def test_lm_head_argmax_fp32(gpu, m):
-    """Tied lm_head E[151936, 2560]: GPU argmax == CPU fp32-score argmax."""
+    """Tied lm_head E[151936, 2560]: GPU argmax == CPU fp32-score argmax, for
+    every M the head serves up to its limit of 16 rows."""
     e = weight(G.vocab_size, G.hidden_size, seed=70)
     h = activations(m, G.hidden_size, seed=700 + m)
     dev = torch.device("cuda:0")
