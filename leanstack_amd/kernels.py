@@ -146,6 +146,8 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
     res_ptr, ldr = (None, 0) if r2 is None else (r2.data_ptr(), ldr)
     if r2 is not None:
         _require_device(r2, "residual")
+    if m == 0:
+        return out  # no rows: nothing to launch (F.linear returns the empty result too)
     if isinstance(workspace, str):
         if workspace != "auto":
             raise ValueError(f"workspace must be 'auto', None or a tensor, not {workspace!r}")
@@ -199,6 +201,8 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weigh
     res_ptr, ldr = (None, 0) if r2 is None else (r2.data_ptr(), ldr)
     if r2 is not None:
         _require_device(r2, "residual")
+    if m == 0:
+        return out
     dev = _one_device(x, (weight.data, "weight"), (nw, "norm_weight"), (out, "out"), (r2, "residual"))
     with torch.cuda.device(dev):
         status = lib.lsk_rmsnorm_linear_bf16(
@@ -330,6 +334,8 @@ def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: i
         raise ValueError(f"norm_weight must be a bfloat16 tensor of {weight.k} values")
     _require_device(hidden, "hidden")
     _require_device(weight.data, "weight")
+    if m == 0:  # no rows: an empty index tensor, as torch.argmax over [0, V] scores gives
+        return out if out is not None else torch.empty((0,), device=hidden.device, dtype=torch.long)
     if workspace is None or workspace.m < m or workspace.v != v or workspace.k != weight.k:
         workspace = LmHeadWorkspace(m, v, weight.k, hidden.device)
     if out is None:
@@ -384,6 +390,8 @@ def lm_head_argmax_noalloc(hidden: torch.Tensor, weight: PackedWeight, out: torc
         raise ValueError(f"logits_out must be a contiguous float32 tensor of {m}x{weight.n}")
     for t, what in ((hidden, "hidden"), (weight.data, "weight"), (out, "out")):
         _require_device(t, what)
+    if m == 0:
+        return out
     dev = _one_device(hidden, (weight.data, "weight"), (out, "out"), (logits_out, "logits_out"))
     with torch.cuda.device(dev):
         status = _lib.load().lsk_lm_head_argmax_noalloc_bf16(

@@ -362,6 +362,26 @@ def test_largest_activation_stride(gpu, m):
         assert_parity(y.cpu(), expect, f"x at stride {stride}, M={m}")
 
 
+def test_zero_rows_give_empty_results(gpu):
+    """No rows in, no rows out, nothing launched: the empty results F.linear
+    and torch.argmax give for a [0, K] input."""
+    dev = torch.device("cuda:0")
+    n, k = 2560, 4096
+    pw = PackedWeight.from_rowmajor(weight(n, k, seed=92).to(dev))
+    x = torch.empty((0, k), device=dev, dtype=torch.bfloat16)
+    y = kernels.linear(x, pw)
+    assert y.shape == (0, n) and y.dtype == torch.bfloat16
+    y = kernels.linear(x, pw, epilogue=_lib.EPI_RESIDUAL_ADD, residual=torch.empty((0, n), device=dev,
+                                                                                   dtype=torch.bfloat16))
+    assert y.shape == (0, n)
+    y = kernels.rmsnorm_linear(x, torch.ones(k, device=dev, dtype=torch.bfloat16), 1e-6, pw)
+    assert y.shape == (0, n)
+    head = PackedWeight.from_rowmajor(weight(64, k, seed=93).to(dev))
+    idx = kernels.lm_head_argmax(x, head)
+    assert idx.shape == (0,) and idx.dtype == torch.long
+    torch.cuda.synchronize()
+
+
 def test_rejects_bad_shapes_before_launch(gpu):
     dev = torch.device("cuda:0")
     pw = PackedWeight.from_rowmajor(weight(64, 64, seed=1).to(dev))
