@@ -673,3 +673,51 @@ def test_prefill_whole_block_epilogue_strides(gpu, case, narrow):
     assert_parity(y, expect, f"{case} narrow={narrow}")
     untouched = torch.cat([y_buf[:y_off].cpu(), rows[:, n_out:].reshape(-1), y_buf[y_off + m * ldy:].cpu()])
     assert bool((untouched == -7.0).all()), "the epilogue wrote outside the output rows"
+
+
+@pytest.mark.parametrize("m", [1, 3, 12])
+@pytest.mark.parametrize("case", ["o_residual", "down_residual", "qkv", "gate_up_silu"])
+def test_decode_narrowest_strides(gpu, case, m):
+    """The decode kernels through the C ABI at the narrowest rows the ABI
+    accepts: x 16-byte aligned at ldx = K + 8, y 8-byte aligned with
+    ldy % 8 == 4, the residual 2-byte aligned with ldr % 8 == 2.  Elements
+    between the rows stay as they were."""
+    dev = torch.device("cuda:0")
+    if case == "gate_up_silu":
+        n, k, layout, epi = 2 * G.intermediate_size, G.hidden_size, _lib.LAYOUT_MFMA16X32_GATEUP, _lib.EPI_SILU_MUL
+        n_out = G.intermediate_size
+    else:
+        n, k = {"o_residual": PROJ["o_proj"], "down_residual": PROJ["down_proj"], "qkv": PROJ["qkv_proj"]}[case]
+        layout, n_out = _lib.LAYOUT_MFMA16X32, n
+        epi = _lib.EPI_RESIDUAL_ADD if case.endswith("residual") else _lib.EPI_NONE
+    w = weight(n, k, seed=98 + m)
+    x = activations(m, k, seed=980 + m)
+    pw = PackedWeight.from_rowmajor(w.to(dev), layout)
+    ldx = k + 8
+    x_buf = torch.zeros((m, ldx), device=dev, dtype=torch.bfloat16)
+    x_buf[:, :k] = x.to(dev)
+    ldy, y_off = n_out + 4, 4
+    y_buf = torch.full((m * ldy + 8,), -7.0, device=dev, dtype=torch.bfloat16)
+    res_ptr, ldr, r = None, 0, None
+    if epi == _lib.EPI_RESIDUAL_ADD:
+        r = activations(m, n, seed=981 + m)
+        ldr, r_off = n + 2, 1
+        r_buf = torch.zeros((m * ldr + 8,), device=dev, dtype=torch.bfloat16)
+        r_buf[r_off:r_off + m * ldr].view(m, ldr)[:, :n] = r.to(dev)
+        res_ptr = r_buf.data_ptr() + 2 * r_off
+    status = _lib.load().lsk_linear_bf16(pw.data.data_ptr(), layout, n, k, x_buf.data_ptr(), m, ldx,
+                                         y_buf.data_ptr() + 2 * y_off, ldy, epi, res_ptr, ldr, None, 0,
+                                         torch.cuda.current_stream().cuda_stream)
+    _lib.check(status, "lsk_linear_bf16")
+    torch.cuda.synchronize()
+    rows = y_buf[y_off:y_off + m * ldy].view(m, ldy).cpu()
+    y = rows[:, :n_out]
+    if epi == _lib.EPI_SILU_MUL:
+        expect = ref.silu_mul(ref.linear(x, w), n_out)
+    elif epi == _lib.EPI_RESIDUAL_ADD:
+        expect = r + ref.linear(x, w)
+    else:
+        expect = ref.linear(x, w)
+    assert_parity(y, expect, f"decode {case} M={m} narrow rows")
+    untouched = torch.cat([y_buf[:y_off].cpu(), rows[:, n_out:].reshape(-1), y_buf[y_off + m * ldy:].cpu()])
+    assert bool((untouched == -7.0).all()), "the kernel wrote outside the output rows"
