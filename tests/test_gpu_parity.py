@@ -721,3 +721,26 @@ def test_decode_narrowest_strides(gpu, case, m):
     assert_parity(y, expect, f"decode {case} M={m} narrow rows")
     untouched = torch.cat([y_buf[:y_off].cpu(), rows[:, n_out:].reshape(-1), y_buf[y_off + m * ldy:].cpu()])
     assert bool((untouched == -7.0).all()), "the kernel wrote outside the output rows"
+
+
+@pytest.mark.parametrize("m", [1, 3, 12])
+def test_lm_head_strided_hidden_rows(gpu, m):
+    """Hidden rows at a stride above K (a view into a wider buffer, read in
+    place): the same indices and bit-identical fp32 logits as contiguous
+    rows, with and without the fused final RMSNorm (M <= 8)."""
+    dev = torch.device("cuda:0")
+    e = weight(G.vocab_size, G.hidden_size, seed=72)
+    h = activations(m, G.hidden_size, seed=720 + m).to(dev)
+    pw = PackedWeight.from_rowmajor(e.to(dev))
+    wide = torch.zeros((m, G.hidden_size + 64), device=dev, dtype=torch.bfloat16)
+    wide[:, 32:32 + G.hidden_size] = h
+    view = wide[:, 32:32 + G.hidden_size]
+    assert view.stride(0) == G.hidden_size + 64 and view.data_ptr() % 16 == 0
+    norms = [None] + ([torch.ones(G.hidden_size, device=dev, dtype=torch.bfloat16) * 1.5] if m <= 8 else [])
+    for nw in norms:
+        la = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
+        lb = torch.empty_like(la)
+        ia = kernels.lm_head_argmax(h, pw, logits_out=la, norm_weight=nw)
+        ib = kernels.lm_head_argmax(view, pw, logits_out=lb, norm_weight=nw)
+        torch.cuda.synchronize()
+        assert torch.equal(ia, ib) and torch.equal(la.view(torch.int32), lb.view(torch.int32)), f"norm={nw is not None}"
