@@ -106,3 +106,33 @@ def test_first_layer_of_the_stack(stack36):
     torch.cuda.synchronize()
     _check_layer(stack, cpu, 0, m, _outputs(stack, m), "one-layer graph")
     assert stack.layers[0].gate_up.layout == _lib.LAYOUT_MFMA16X32_GATEUP
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("m", [1, 8])
+def test_36_layer_graph_with_rmsnorms_matches_oracle(stack36, m, fused):
+    """The step with the two RMSNorms of each layer (input_layernorm in front
+    of QKV, post_attention_layernorm in front of gate_up,
+    qwen_explicit.py:1255 and :941), fused into those kernels or run as
+    F.rms_norm launches, captured as one graph: the last layer's outputs
+    against the oracle's norm then projection."""
+    stack, cpu = stack36
+    for t in (stack.y_qkv, stack.y_o, stack.act, stack.y_down):
+        t.fill_(float("nan"))
+    graph = stack.capture(lambda: stack.launch_with_norms(m, fused))
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    got = _outputs(stack, m)
+    del graph
+    layer = G.num_hidden_layers - 1
+    ln_in, ln_post = (stack.norm_w[layer, i].cpu() for i in (0, 1))
+    x_qkv, x_o, x_gu = (t[layer, :m].cpu() for t in (stack.x_qkv, stack.x_o, stack.x_gu))
+    y_qkv = ref.linear(ref.rmsnorm(x_qkv, ln_in, stack.eps), cpu[(layer, "qkv_proj")])
+    y_o = ref.linear(x_o, cpu[(layer, "o_proj")])
+    act = ref.silu_mul(ref.linear(ref.rmsnorm(x_gu, ln_post, stack.eps), cpu[(layer, "gate_up_proj")]),
+                       G.intermediate_size)
+    what = f"{'fused' if fused else 'separate'} norms, layer {layer} M={m}"
+    for name, g, e in zip(("qkv", "o", "act"), got[:3], (y_qkv, y_o, act)):
+        assert_parity(g.cpu(), e, f"{what} {name}")
+    assert_parity(got[3].cpu(), ref.linear(act, cpu[(layer, "down_proj")]), f"{what} down")
