@@ -136,3 +136,20 @@ def test_36_layer_graph_with_rmsnorms_matches_oracle(stack36, m, fused):
     for name, g, e in zip(("qkv", "o", "act"), got[:3], (y_qkv, y_o, act)):
         assert_parity(g.cpu(), e, f"{what} {name}")
     assert_parity(got[3].cpu(), ref.linear(act, cpu[(layer, "down_proj")]), f"{what} down")
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_36_layer_persistent_step_matches_oracle(stack36, m):
+    """The same 144-projection step as one persistent launch (the chained
+    stack program the bench also times): no wait gives up, and the last
+    layer's outputs meet the oracle (the persistent kernel sums in another
+    order than the launch kernels, so parity, not bit equality, is the bar)."""
+    stack, cpu = stack36
+    for t in (stack.y_qkv, stack.y_o, stack.act, stack.y_down):
+        t.fill_(float("nan"))
+    step = stack.persistent_step(m, chain=True)
+    step.launch()
+    torch.cuda.synchronize()
+    assert step.error() == 0
+    _check_layer(stack, cpu, G.num_hidden_layers - 1, m, _outputs(stack, m), "persistent")
+    del step
