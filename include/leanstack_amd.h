@@ -107,8 +107,12 @@ int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* 
  * block of the prefill block GEMM (256, 192 or 128), plan[1] = output blocks,
  * plan[2] = blocks whose K range is split over several workgroups, plan[3] =
  * workgroups (K chunks) per split block (1: no split).  plan = {0, 0, 0, 1}
- * when the call takes the decode kernels (M <= 16, or a shape off the block
- * GEMM's tile grid) or the plain 128-row GEMM.  A workspace smaller than
+ * whenever the call takes another kernel than the block GEMM, and the plan
+ * does not say which: the decode kernels (M <= 16, or N or K off every GEMM
+ * tile grid), the 256x256 GEMM with both operands staged in LDS (M > 128,
+ * N % 256 == 0, K % 64 == 0 but not a shape the block GEMM takes, e.g. K an
+ * odd multiple of 64) or the 128x128 GEMM (the rest of M = 17..128 and of
+ * N % 128 == 0, K % 64 == 0).  A workspace smaller than
  * lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K) is refused with
  * LSK_ERR_WORKSPACE, as lsk_linear_bf16 refuses it.  For tests and tuning; no
  * counterpart in the reference, whose F.linear hides its cuBLAS plan. */

@@ -652,6 +652,9 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][TB], const Args& g, 
   // reads and its global traffic (4A weight loads in step 0, 8 DMA in
   // step 1).
   constexpr int kM = A * TB;
+  // Step 1's 8 DMAs go after the MFMAs that follow its TB LDS reads, as far
+  // as the step has MFMAs there: for A = 1 (kM = TB = 8) from the first one.
+  constexpr int kDmaSlot = kM - 8 >= TB ? TB : (kM > 8 ? kM - 8 : 0);
   // Stage s multiplies buffer cur, DMAs the activations of stage s + 2 into
   // dst (the buffer stage s - 1 read) and, before its barrier, waits for the
   // DMA of stage s + 1 (issued one stage earlier; only the 4A weight loads
@@ -671,7 +674,7 @@ __device__ __forceinline__ void mainloop(f32x16_t (&acc)[A][TB], const Args& g, 
     read_b(fb0, cur, 2);
     dma_x(dst, xr, g.ldx, rmax, sx, wave, lane);
     mfma_step(wc.v[1], fb1);
-    sched_step<kM, TB, TB, 8>();
+    sched_step<kM, TB, kDmaSlot, 8>();
 
     __builtin_amdgcn_sched_barrier(0);
     read_b(fb1, cur, 3);

@@ -65,29 +65,35 @@ def _device_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
-def _device_workspace(cache: dict[int, torch.Tensor], device: torch.device, nbytes: int, what: str) -> torch.Tensor:
-    """The zero-filled workspace of `cache` for `device`, grown to `nbytes`.
-    One per device: calls that share it must be stream-ordered.  It is never allocated
-    while the stream is being captured, so a captured graph never replays a
-    workspace's allocation or zero fill."""
-    key = _device_index(device)
+def _device_workspace(cache: dict[tuple[int, int], torch.Tensor], device: torch.device, nbytes: int,
+                      what: str) -> torch.Tensor:
+    """The zero-filled workspace of `cache` for `device` and the current
+    stream, grown to `nbytes`.  One per (device, stream): the split blocks of
+    a call count arrivals in the workspace's flag words and read each other's
+    partial slots, so two calls that overlap must not share one, and calls on
+    one stream are ordered.  It is never allocated while the stream is being
+    captured, so a captured graph never replays a workspace's allocation or
+    zero fill (run the same launch once on the capture stream before the
+    capture); a graph keeps using the workspace of the stream it was captured
+    on, so eager calls on that stream must not overlap its replays."""
+    key = (_device_index(device), torch.cuda.current_stream(device).cuda_stream)
     ws = cache.get(key)
     if ws is None or ws.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f"the {what} workspace must be allocated before graph capture: run the same "
-                               f"launch once outside the capture first")
+                               f"launch once on the capture stream, outside the capture, first")
         ws = torch.zeros(nbytes, device=device, dtype=torch.uint8)
         cache[key] = ws
     return ws
 
 
-_prefill_workspaces: dict[int, torch.Tensor] = {}
+_prefill_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def prefill_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor | None:
-    """The split-K workspace of the prefill GEMM on `device` (zero-filled
-    once, left zero-filled by every call), or None when the shape does not
-    use one."""
+    """The split-K workspace of the prefill GEMM on `device` for the current
+    stream (zero-filled once, left zero-filled by every call), or None when
+    the shape does not use one."""
     nbytes = _lib.load().lsk_workspace_bytes(_lib.OP_LINEAR, m, n, k)
     if nbytes == 0:
         return None
@@ -118,8 +124,8 @@ def linear(x: torch.Tensor, weight: PackedWeight, *, epilogue: int = _lib.EPI_NO
 
     epilogue EPI_NONE (N' = N), EPI_SILU_MUL (gate_up layout, N' = N/2,
     SiLU(gate)*up), EPI_RESIDUAL_ADD (N' = N, residual + projection).
-    workspace: "auto" uses the device's split-K workspace for prefill shapes
-    (prefill_workspace; for calls ordered on one stream), None runs one
+    workspace: "auto" uses the split-K workspace of the device and current
+    stream for prefill shapes (prefill_workspace), None runs one
     workgroup per output block with no waits (the form for prefill calls
     that may run concurrently with other kernels on the device), a uint8
     device tensor is used as given.  A split-K workgroup whose bounded wait
@@ -216,14 +222,14 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, weigh
     return out
 
 
-_attention_workspaces: dict[int, torch.Tensor] = {}
+_attention_workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def attention_workspace(device: torch.device, n_q: int, n_kv: int, head_dim: int,
                         max_seq_len: int) -> torch.Tensor:
-    """The decode attention workspace of `device` (zero-filled once, left
-    zero-filled by every call), large enough for this geometry.  Calls
-    sharing it must be stream-ordered."""
+    """The decode attention workspace of `device` for the current stream
+    (zero-filled once, left zero-filled by every call), large enough for this
+    geometry.  Calls on other streams get their own."""
     nbytes = _lib.load().lsk_attention_workspace_bytes(n_q, n_kv, head_dim, max_seq_len)
     if nbytes == 0:
         raise ValueError(f"no attention workspace for n_q={n_q}, n_kv={n_kv}, head_dim={head_dim}, "

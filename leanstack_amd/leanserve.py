@@ -14,6 +14,8 @@ resident with room to spare.
 
 from __future__ import annotations
 
+import json
+import struct
 from dataclasses import dataclass, field
 from pathlib import Path
 from math import ceil
@@ -360,6 +362,24 @@ class _RegionReader:
                 ev.synchronize()
 
 
+def _safetensors_data_offsets(path: Path) -> dict[str, tuple[int, int]]:
+    """Absolute byte range of every tensor in a safetensors file, read from
+    its header (8-byte little-endian header length, JSON header whose
+    `data_offsets` are relative to the data region that follows it)."""
+    with open(path, "rb") as f:
+        head = f.read(8)
+        if len(head) != 8:
+            raise ValueError(f"{path}: truncated (no safetensors header)")
+        (hlen,) = struct.unpack("<Q", head)
+        raw = f.read(hlen)
+    if len(raw) != hlen:
+        raise ValueError(f"{path}: truncated safetensors header")
+    header = json.loads(raw)
+    base = 8 + hlen
+    return {name: (base + int(v["data_offsets"][0]), base + int(v["data_offsets"][1]))
+            for name, v in header.items() if name != "__metadata__"}
+
+
 def load_pack_into_arena(root: Path, manifest, arena: "ResidentArena") -> dict[str, int]:
     """Fill every planned weight of `arena` from the pack at `root` by
     direct file offsets.  A file whose tensors sit at the same relative
@@ -382,6 +402,18 @@ def load_pack_into_arena(root: Path, manifest, arena: "ResidentArena") -> dict[s
     missing = sorted(planned - {t.name for ts in by_file.values() for t in ts})
     if missing:
         raise ValueError(f"{root}: the pack has no tensor for {len(missing)} planned weights, e.g. {missing[:3]}")
+    # The manifest's offsets must name the bytes the safetensors header
+    # itself gives each tensor: a wrong offset would load another tensor's
+    # bytes (or the header) with every size check still passing.
+    for file_name, ts in by_file.items():
+        ranges = _safetensors_data_offsets(root / file_name)
+        for t in ts:
+            if t.name not in ranges:
+                raise ValueError(f"{root / file_name}: no tensor {t.name} in the safetensors header")
+            lo, hi = ranges[t.name]
+            if (lo, hi - lo) != (t.file_offset_bytes, t.size_bytes):
+                raise ValueError(f"{t.name}: the manifest places it at file offset {t.file_offset_bytes} "
+                                 f"({t.size_bytes} bytes), the safetensors header at {lo} ({hi - lo} bytes)")
     largest = max(ts[-1].file_offset_bytes + ts[-1].size_bytes - ts[0].file_offset_bytes
                   for ts in (sorted(v, key=lambda t: t.file_offset_bytes) for v in by_file.values()))
     reader = _RegionReader(arena, largest)

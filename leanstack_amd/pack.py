@@ -73,7 +73,7 @@ class PackedTensorEntry:
     logical_offset_bytes: int   # offset inside the file's data region (aligned)
     size_bytes: int
     source_tensors: list[str]
-    file_offset_bytes: int = 0  # absolute byte offset of the data in the file (FILE_ALIGNMENT aligned)
+    file_offset_bytes: int      # absolute byte offset of the data in the file (FILE_ALIGNMENT aligned)
 
 
 @dataclass(frozen=True)
@@ -211,6 +211,12 @@ def load_packed_artifact_manifest(path_or_dir: str | Path) -> PackedArtifactMani
     fmt = payload.get("format_version")
     if fmt != FORMAT_VERSION:
         raise ValueError(f"{path}: format {fmt!r} is not {FORMAT_VERSION} (repack the checkpoint with this packer)")
+    for t in payload.get("tensors", []):
+        # An early leanpack/v1 writer left this field out; the loader reads
+        # every tensor at this offset, so a manifest without it is refused.
+        if not isinstance(t.get("file_offset_bytes"), int) or t["file_offset_bytes"] < 0:
+            raise ValueError(f"{path}: tensor {t.get('name')!r} has no file_offset_bytes "
+                             f"(written by an older packer; repack the checkpoint with this packer)")
     manifest = PackedArtifactManifest.from_payload(payload)
     known = set(LAYOUT_NAMES.values()) | {"rowmajor"}
     for t in manifest.tensors:

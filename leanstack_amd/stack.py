@@ -125,15 +125,20 @@ class DecodeLinearStack:
         return kernels.StackStep(specs, m, self.device)
 
     def capture(self, fn) -> torch.cuda.CUDAGraph:
-        """Capture `fn()` (a launch sequence) as a HIP graph."""
-        side = torch.cuda.Stream(device=self.device)
+        """Capture `fn()` (a launch sequence) as a HIP graph.  The warm-up
+        run and the capture use the stack's own capture stream, so workspaces
+        that kernels.linear keeps per (device, stream) exist before the
+        capture and no other work shares them."""
+        if getattr(self, "_capture_stream", None) is None:
+            self._capture_stream = torch.cuda.Stream(device=self.device)
+        side = self._capture_stream
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):
             fn()  # warm the launch path outside capture
         torch.cuda.current_stream(self.device).wait_stream(side)
         torch.cuda.synchronize(self.device)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=side):
             fn()
         torch.cuda.synchronize(self.device)
         return graph

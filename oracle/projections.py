@@ -90,9 +90,3 @@ def bf16_logits_argmax(hidden: torch.Tensor, lm_w: torch.Tensor) -> torch.Tensor
     h = hidden.view(-1, hidden.shape[-1])
     logits = torch.stack([torch.mv(lm_w, h[i]) for i in range(h.shape[0])])
     return logits.argmax(dim=-1)
-
-
-def top2_margin(scores: torch.Tensor) -> torch.Tensor:
-    """Gap between the largest and second-largest score per row (fp32)."""
-    top = torch.topk(scores.float(), 2, dim=-1).values
-    return top[..., 0] - top[..., 1]

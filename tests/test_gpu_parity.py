@@ -37,6 +37,43 @@ def _gpu_linear(x, w, layout=_lib.LAYOUT_MFMA16X32, epilogue=_lib.EPI_NONE, resi
     return y.cpu()
 
 
+# The reference's hot-kernel GEMM cases (src/leanstack/hot_kernels.py:79-166):
+# key -> (M, N, K).  gate_up there is one half of the fused projection (no
+# SiLU); q_proj and kv_proj are the row slices of the fused QKV.
+HOT_KERNEL_CASES = {
+    "q_proj_prefill64": (64, 4096, 2560),
+    "q_proj_prefill1024": (1024, 4096, 2560),
+    "kv_proj_prefill64": (64, 1024, 2560),
+    "o_proj_prefill64": (64, 2560, 4096),
+    "gate_up_proj_prefill64": (64, 9728, 2560),
+    "down_proj_prefill64": (64, 2560, 9728),
+}
+
+
+@pytest.mark.parametrize("case", sorted(HOT_KERNEL_CASES))
+def test_reference_hot_kernel_cases(gpu, case):
+    """Every GEMM case of the reference's hot-kernel table at its own M
+    (64, and 1024 for q_proj) against the oracle's F.linear."""
+    m, n, k = HOT_KERNEL_CASES[case]
+    w = weight(n, k, seed=70 + n % 97)
+    x = activations(m, k, seed=71)
+    assert_parity(_gpu_linear(x, w), ref.linear(x, w), case)
+
+
+def test_auto_workspaces_are_per_stream(gpu):
+    """workspace="auto" keeps one split-K workspace per (device, stream):
+    calls on another stream never share the arrival flags and partial slots
+    of a call that may overlap them."""
+    dev = torch.device("cuda:0")
+    a = kernels.prefill_workspace(dev, 2048, 2560, 4096)
+    other = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(other):
+        b = kernels.prefill_workspace(dev, 2048, 2560, 4096)
+    assert a is not None and b is not None
+    assert a.data_ptr() != b.data_ptr()
+    assert kernels.prefill_workspace(dev, 2048, 2560, 4096).data_ptr() == a.data_ptr()
+
+
 def test_o_proj_gemv_config1(gpu):
     """x[1,4096] ~ N(0,1), W[2560,4096] ~ N(0,0.02): elementwise within bf16
     rounding + the fp32 summation bound of the float64 brute force."""

@@ -7,9 +7,9 @@ builds it -- 36 distinct random N(0, 0.02) layers packed into one resident
 arena, fresh N(0, 1) inputs per layer -- captured as one HIP graph and
 replayed.  Every layer writes the same output buffers, so after a replay
 they hold the last layer's projections, and down_proj reads the activation
-that layer's gate_up kernel wrote: the oracle recomputes that layer (and the
-first, through a one-layer graph) from the CPU copies of its weights at the
-parity bar.  The graph's outputs also equal an eager launch of the same
+that layer's gate_up kernel wrote: the oracle recomputes that layer (and
+layers 0, 1, 17 and 34, through one-layer graphs of the same arena) from the
+CPU copies of their weights at the parity bar.  The graph's outputs also equal an eager launch of the same
 sequence bit for bit.  The reference's callers are run_semantic_stack_decode /
 run_semantic_stack_verify_from_hidden (src/leanstack/runtime/
 qwen_explicit.py:1617-1644, :1676-1716).
@@ -30,11 +30,15 @@ from tests.helpers import assert_parity
 pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda:0")
+# layers checked through one-layer graphs of the arena (the full step's
+# outputs hold only the last layer's)
+CHECKED_LAYERS = (0, 1, 17, 34)
 
 
 @pytest.fixture(scope="module")
 def stack36(gpu):
-    """The bench's 36-layer arena, with CPU copies of layers 0 and 35."""
+    """The bench's 36-layer arena, with CPU copies of layers 0, 1, 17, 34
+    and 35."""
     plan = build_resident_buffer_plan(G, max_rows=16, include_embedding=False, include_lm_head=False, buckets=())
     arena = ResidentArena(plan, DEV)
     gen = torch.Generator(device=DEV).manual_seed(0)
@@ -45,7 +49,7 @@ def stack36(gpu):
         for proj, (n, k) in G.projections().items():
             w = (torch.randn((n, k), generator=gen, device=DEV) * 0.02).to(torch.bfloat16)
             arena.store_rowmajor(names[proj], w)
-            if l in (0, last):
+            if l in CHECKED_LAYERS + (last,):
                 cpu[(l, proj)] = w.cpu()
             del w
         layers.append(LayerProjections(arena.packed(names["qkv_proj"]), arena.packed(names["o_proj"]),
@@ -96,16 +100,21 @@ def test_36_layer_graph_matches_oracle(stack36, m):
         assert torch.equal(g.view(torch.int16), e.view(torch.int16))
 
 
-def test_first_layer_of_the_stack(stack36):
-    """Layer 0 through a one-layer graph of the same launches (its outputs are
-    overwritten by the later layers in the full step)."""
+@pytest.mark.parametrize("layer", CHECKED_LAYERS)
+def test_single_layers_of_the_stack(stack36, layer):
+    """Layers 0, 1, 17 and 34 through one-layer graphs of the same launches
+    on the same arena (their outputs are overwritten by the later layers in
+    the full step): every layer's arena views and kernels, not only the
+    last one's, meet the oracle."""
     stack, cpu = stack36
     m = 4
-    graph = stack.capture(lambda: stack.launch(m, range(0, 1)))
+    for t in (stack.y_qkv, stack.y_o, stack.act, stack.y_down):
+        t.fill_(float("nan"))
+    graph = stack.capture(lambda: stack.launch(m, range(layer, layer + 1)))
     graph.replay()
     torch.cuda.synchronize()
-    _check_layer(stack, cpu, 0, m, _outputs(stack, m), "one-layer graph")
-    assert stack.layers[0].gate_up.layout == _lib.LAYOUT_MFMA16X32_GATEUP
+    _check_layer(stack, cpu, layer, m, _outputs(stack, m), "one-layer graph")
+    assert stack.layers[layer].gate_up.layout == _lib.LAYOUT_MFMA16X32_GATEUP
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -138,7 +147,7 @@ def test_36_layer_graph_with_rmsnorms_matches_oracle(stack36, m, fused):
     assert_parity(got[3].cpu(), ref.linear(act, cpu[(layer, "down_proj")]), f"{what} down")
 
 
-@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
 def test_36_layer_persistent_step_matches_oracle(stack36, m):
     """The same 144-projection step as one persistent launch (the chained
     stack program the bench also times): no wait gives up, and the last

@@ -209,6 +209,37 @@ def test_loader_refuses_a_mislabelled_layout(tiny_pack, tmp_path):
         materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
 
 
+def test_loader_refuses_a_manifest_without_file_offsets(tiny_pack, tmp_path):
+    """An early leanpack/v1 manifest had no file_offset_bytes; reading each
+    tensor at offset 0 would load the safetensors header as weights with
+    every size check passing, so such a manifest is refused."""
+    _, out, _ = tiny_pack
+
+    def strip(payload):
+        for t in payload["tensors"]:
+            t.pop("file_offset_bytes", None)
+
+    bad = _copy_pack(out, tmp_path / "nooffsets", strip)
+    with pytest.raises(ValueError, match="no file_offset_bytes"):
+        materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
+
+
+def test_loader_refuses_an_offset_the_header_contradicts(tiny_pack, tmp_path):
+    """An offset that points at another tensor's (aligned, same-sized)
+    bytes passes the layout and size checks; the safetensors header names
+    the true range, and the loader holds the manifest to it."""
+    _, out, _ = tiny_pack
+
+    def shift(payload):
+        for t in payload["tensors"]:
+            if t["name"] == "layers.0.attention.o_proj.weight":
+                t["file_offset_bytes"] += 4096
+
+    bad = _copy_pack(out, tmp_path / "shifted", shift)
+    with pytest.raises(ValueError, match="the safetensors header at"):
+        materialize_qwen_semantic_stack_from_leanpack(bad, device="cpu", buckets=())
+
+
 @pytest.mark.gpu
 def test_real_shape_layer_from_pack_runs_the_dispatch_path(gpu, tmp_path):
     from leanstack_amd import dispatch

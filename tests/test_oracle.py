@@ -171,6 +171,45 @@ def test_logits_argmax_planted_and_ties():
     assert ref.logits_argmax(ht, from_bits(w)).item() == 300
 
 
+def test_greedy_head_vector_applies_the_final_norm_weight():
+    """RMSNorm is scale-invariant for the argmax, so a tie test with an
+    all-ones weight cannot see the final norm weight.  Here the weight is 4
+    on the first half of the hidden dims and 1/4 on the second half, and two
+    vocab rows each read one half (the second with 4x the magnitude):
+    applied as rmsnorm(h) * w, row 0 wins (4 x 32 against 4 x 0.25 x 32);
+    dropped, row 1 wins (128 against 32); divided instead of multiplied or
+    applied to the swapped halves, row 1 wins too.  A random case is held to
+    the float64 chain of the reference (qwen_explicit.py:952-960)."""
+    k = 64
+    h = torch.ones(k, dtype=torch.bfloat16)
+    w_norm = torch.cat((torch.full((k // 2,), 4.0), torch.full((k // 2,), 0.25))).to(torch.bfloat16)
+    lm = torch.zeros((3, k), dtype=torch.float32)
+    lm[0, : k // 2] = 1.0
+    lm[1, k // 2:] = 4.0
+    lm[2] = -1.0
+    lm = lm.to(torch.bfloat16)
+    assert ref.greedy_head_vector(h, w_norm, lm, 1e-6).item() == 0
+    # the plausible mistakes pick row 1
+    assert ref.greedy_head_vector(h, torch.ones(k, dtype=torch.bfloat16), lm, 1e-6).item() == 1
+    assert ref.greedy_head_vector(h, (1.0 / w_norm.float()).to(torch.bfloat16), lm, 1e-6).item() == 1
+    assert ref.greedy_head_vector(h, w_norm.flip(0), lm, 1e-6).item() == 1
+
+    rng = np.random.default_rng(12)
+    v, k = 1024, 256
+    lm_bits = brute.f32_to_bf16_bits((rng.standard_normal((v, k)) * 0.02).astype(np.float32))
+    h_bits = brute.f32_to_bf16_bits((rng.standard_normal(k) * 2.0).astype(np.float32))
+    wn_bits = brute.f32_to_bf16_bits((1.0 + 0.5 * rng.standard_normal(k)).astype(np.float32))
+    h64, wn64, lm64 = (brute.bf16_bits_to_f64(b) for b in (h_bits, wn_bits, lm_bits))
+    normed = brute.round_bf16(h64 / np.sqrt(np.mean(h64 * h64) + 1e-6) * wn64)
+    logits = lm64 @ normed
+    top = np.sort(logits)[-2:]
+    got = ref.greedy_head_vector(from_bits(h_bits[None])[0], from_bits(wn_bits[None])[0], from_bits(lm_bits),
+                                 1e-6).item()
+    # bf16 logits may merge scores closer than one bf16 step at their size
+    assert top[1] - top[0] > 2 * brute.bf16_ulp(np.array([top[1]]))[0]
+    assert got == int(np.argmax(logits))
+
+
 def test_logits_scores_are_fp32_accumulated():
     """The cuTile head accumulates f32(W) * f32(h) in fp32 (cutile_logits.py:27):
     the oracle's scores stay within the fp32 summation bound of float64."""
