@@ -84,21 +84,6 @@ def profiled_mfma_util() -> float | None:
     return prefill_profile().get("mfma_util_pct_m2048")
 
 
-def loaded_clock_peak_tflops(m: int) -> dict | None:
-    """Dense BF16 MFMA peak at the shader clock the committed profile measured
-    under this prefill load (GRBM_GUI_ACTIVE / duration, time-weighted over
-    the four projections at M = m): 256 CUs x 4 SIMDs x 1024 FLOP/clk x f.
-    The published 2.5 PFLOP/s assumes 2.4 GHz; the chip holds less under
-    sustained MFMA load."""
-    prof = prefill_profile()
-    clocks = prof.get(f"clock_ghz_m{m}")
-    weights = prof.get(f"us_m{m}")
-    if not clocks or not weights:
-        return None
-    ghz = sum(clocks[k] * weights[k] for k in clocks) / sum(weights[k] for k in clocks)
-    return {"clock_ghz": round(ghz, 3), "peak": round(256 * 4 * 1024 * ghz * 1e9 / 1e12, 1)}
-
-
 def measured_traffic(kernel_label: str):
     """HBM bytes per launch of the roofline kernel, as the committed counter
     profile measured it (profiles/hbm_traffic.json), or None."""
@@ -225,6 +210,44 @@ HOT_KERNEL_CASES = {
 }
 
 
+ROOF_KERNEL = "decode_half_kernel<4,2,1,10,-3> (gate_up 19456x2560 + silu*up, M=1)"
+PREFILL_ROOF_KERNEL = "gemm_wdx_kernel (qkv, o, gate_up + silu*up, down at 2048 tokens)"
+PREFILL_REPS = 8  # launches per graph replay: back to back, as the layers of a prefill run
+
+
+def prefill_graph_times(torch, kernels, lib, stack, layer, m: int, steps: int, gen, dev) -> dict[str, float]:
+    """Microseconds per launch of each prefill projection at m tokens (split-K
+    workspace): PREFILL_REPS launches per graph replay, so the graph's own
+    launch cost is not counted against one GEMM; HIP events on the replay
+    stream around max(3, steps // 2) replays after 2 warm-ups."""
+    weights = {"qkv_proj": layer.qkv, "o_proj": layer.o, "gate_up_proj": layer.gate_up, "down_proj": layer.down}
+    out = {}
+    for name, pw in weights.items():
+        x = torch.randn((m, pw.k), generator=gen, device=dev).to(torch.bfloat16)
+        epi = lib.EPI_SILU_MUL if name == "gate_up_proj" else lib.EPI_NONE
+        y = torch.empty((m, pw.out_features), device=dev, dtype=torch.bfloat16)
+        graph = stack.capture(lambda x=x, pw=pw, epi=epi, y=y: [
+            kernels.linear(x, pw, epilogue=epi, out=y) for _ in range(PREFILL_REPS)])
+        out[name] = time_graph(torch, graph, max(3, steps // 2), 2) * 1e3 / PREFILL_REPS
+        del graph, x, y
+    return out
+
+
+def step_kernel_durations(kernels, stack, g, reps: int) -> dict[str, list[float]]:
+    """Each dispatch's own duration (us) over `reps` eager launches of the
+    36-layer M = 1 step, by projection (the step launches qkv, o, gate_up,
+    down per layer, in that order).  The events are bound to the dispatches
+    themselves (lsk_dispatch_timing_begin/end), so these are the kernels'
+    execution times with the GPU idle between launches."""
+    durs = kernels.kernel_durations_us(lambda: [stack.launch(1) for _ in range(reps)],
+                                       max_dispatches=4 * g.num_hidden_layers * reps)
+    return {name: durs[i::4] for i, name in enumerate(g.projections())}
+
+
+def mean(values: list[float]) -> float:
+    return sum(values) / len(values)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -236,6 +259,11 @@ def main() -> int:
                     help="short run for hardware-counter profiling: a 1 GiB copy of known size, then each "
                          "projection kind once per layer, the QKV and gate_up kernels with the RMSNorm prologue "
                          "once per layer, and the lm_head once, no graphs")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the two roofline measurements of the default run (the gate_up decode kernel over "
+                         "36-launch graph replays, the four prefill GEMMs at M = 2048 over 8-launch replays), for "
+                         "profiling with rocprofv3 --kernel-trace --stats: the trace then holds exactly their "
+                         "dispatches")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
                          "M = 2048 and 8192, three launches each, no graphs")
@@ -282,6 +310,30 @@ def main() -> int:
     log(f"arena {plan.arena_bytes / 1e9:.2f} GB resident in {time.perf_counter() - t0:.1f} s")
 
     stack = DecodeLinearStack(layers, G, max_rows=16, device=dev)
+
+    if args.roofline_only:
+        # The default run's two roofline measurements and nothing else, so a
+        # kernel trace of this command holds exactly their dispatches.
+        graph = stack.capture(lambda: stack.launch_projection("gate_up_proj", 1))
+        settle(torch, graph)
+        ms = time_graph(torch, graph, steps, warmup)
+        del graph
+        us = ms * 1e3 / G.num_hidden_layers
+        bytes_gu = G.projection_bytes("gate_up_proj", 1)
+        pre = prefill_graph_times(torch, kernels, _lib, stack, layers[0], 2048, steps, gen, dev)
+        layer_us = sum(pre.values())
+        print(json.dumps({
+            "roofline_only": True,
+            "roofline": {"kernel": ROOF_KERNEL, "us_per_launch": round(us, 3),
+                         "launches": G.num_hidden_layers * (steps + warmup),
+                         "achieved": round(bytes_gu / (us * 1e-6) / 1e9, 1),
+                         "frac": round(bytes_gu / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+            "roofline_prefill": {"kernel": PREFILL_ROOF_KERNEL, "layer_us": round(layer_us, 2),
+                                 "us_per_launch": {n: round(v, 3) for n, v in pre.items()},
+                                 "frac": round(G.layer_flops(2048) / (layer_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS,
+                                               4)},
+        }), flush=True)
+        return 0
 
     if args.pmc:
         # Calibration: a plain device copy of exactly 1 GiB (read 1 GiB, write 1 GiB).
@@ -405,11 +457,19 @@ def main() -> int:
         }
         log(f"{name} M=1: {us:.2f} us/launch, {per_kernel[name]['GB/s']} GB/s")
         del graph
-    # Dominant kernel of the launch graph: the fused gate_up + SiLU*up decode
-    # kernel (49% of the step's bytes), timed over 36 launches.
-    roof_kernel = "decode_half_kernel<4,2,1,10,-3> (gate_up 19456x2560 + silu*up, M=1)"
+    # Dominant kernel of the step: the fused gate_up + SiLU*up decode kernel
+    # (49% of the step's bytes), per launch over 36 back-to-back launches.
+    roof_kernel = ROOF_KERNEL
     roof_bytes = G.projection_bytes("gate_up_proj", 1)
-    achieved = roof_bytes / (per_kernel["gate_up_proj"]["us_per_launch"] * 1e-6) / 1e9
+    roof_us = per_kernel["gate_up_proj"]["us_per_launch"]
+    achieved = roof_bytes / (roof_us * 1e-6) / 1e9
+    # The same kernels launched eagerly, one dispatch at a time, each timed
+    # by events bound to the dispatch itself: their own durations with the
+    # GPU idle between launches (slower than back to back in a graph).
+    step_durs = step_kernel_durations(kernels, stack, G, 2)
+    for name, v in step_durs.items():
+        per_kernel[name]["eager_kernel_us"] = round(mean(v), 3)
+        log(f"{name} M=1 eager dispatch: {mean(v):.3f} us kernel time")
 
     # --- lm_head + argmax ------------------------------------------------------
     head = {}
@@ -429,27 +489,13 @@ def main() -> int:
     # --- prefill GEMMs ---------------------------------------------------------
     prefill = {}
     if not args.quick:
-        p0 = layers[0]
-        weights = {"qkv_proj": p0.qkv, "o_proj": p0.o, "gate_up_proj": p0.gate_up, "down_proj": p0.down}
         for m in (512, 2048, 8192):
-            row = {}
-            layer_ms = 0.0
-            for name, pw in weights.items():
-                x = torch.randn((m, pw.k), generator=gen, device=dev).to(torch.bfloat16)
-                epi = _lib.EPI_SILU_MUL if name == "gate_up_proj" else _lib.EPI_NONE
-                y = torch.empty((m, pw.out_features), device=dev, dtype=torch.bfloat16)
-                # 8 launches per replay: back to back, as the layers of a prefill run,
-                # so the graph's own launch cost is not counted against one GEMM.
-                reps = 8
-                graph = stack.capture(lambda x=x, pw=pw, epi=epi, y=y, r=reps: [
-                    kernels.linear(x, pw, epilogue=epi, out=y) for _ in range(r)])
-                ms = time_graph(torch, graph, max(3, steps // 2), 2) / reps
-                layer_ms += ms
-                tflops = G.projection_flops(name, m) / (ms * 1e-3) / 1e12
-                row[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 1)}
-                del graph, x, y
-            row["layer_us"] = round(layer_ms * 1e3, 1)
-            row["layer_TFLOP/s"] = round(G.layer_flops(m) / (layer_ms * 1e-3) / 1e12, 1)
+            times = prefill_graph_times(torch, kernels, _lib, stack, layers[0], m, steps, gen, dev)
+            row = {name: {"us": round(us, 1), "TFLOP/s": round(G.projection_flops(name, m) / (us * 1e-6) / 1e12, 1)}
+                   for name, us in times.items()}
+            layer_us = sum(times.values())
+            row["layer_us"] = round(layer_us, 1)
+            row["layer_TFLOP/s"] = round(G.layer_flops(m) / (layer_us * 1e-6) / 1e12, 1)
             prefill[m] = row
             log(f"prefill M={m}: layer {row['layer_us']} us, {row['layer_TFLOP/s']} TFLOP/s")
 
@@ -479,22 +525,18 @@ def main() -> int:
         achieved_tf = row["layer_TFLOP/s"]
         prefill_roofline = {
             "bound": "mfma",
-            "kernel": "gemm_wdx_kernel (qkv, o, gate_up + silu*up, down at 2048 tokens)",
+            "kernel": PREFILL_ROOF_KERNEL,
             "flops_per_layer": G.layer_flops(2048),
             "achieved": achieved_tf,
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved_tf / BF16_PEAK_TFLOPS, 4),
             "layer_us": row["layer_us"],
+            "us_per_launch": {n: row[n]["us"] for n in G.projections()},
             "per_projection_TFLOP/s": {n: row[n]["TFLOP/s"] for n in G.projections()},
             "mfma_util_pct": profiled_mfma_util(),
             "mfma_util_source": "profiles/prefill_gemm_counters.md (rocprofv3 --pmc MfmaUtil, bench.py --pmc-prefill)",
         }
-        loaded = loaded_clock_peak_tflops(2048)
-        if loaded is not None:
-            prefill_roofline["peak_at_loaded_clock"] = loaded["peak"]
-            prefill_roofline["loaded_clock_ghz"] = loaded["clock_ghz"]
-            prefill_roofline["frac_at_loaded_clock"] = round(achieved_tf / loaded["peak"], 4)
 
     cpu = None
     if not args.quick:
@@ -529,6 +571,10 @@ def main() -> int:
             "bound": "hbm",
             "kernel": roof_kernel,
             "bytes_per_launch": roof_bytes,
+            "us_per_launch": round(roof_us, 3),
+            "us_per_launch_source": (f"HIP events on the replay stream around {steps} replays of a graph of "
+                                     f"{G.num_hidden_layers} back-to-back launches (one per layer), after {warmup} "
+                                     f"warm-up replays"),
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

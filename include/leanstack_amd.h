@@ -334,6 +334,20 @@ int lsk_linear_error(void* workspace, int* error_out);
  * reference, whose library GEMMs have no cross-workgroup waits. */
 void lsk_set_linear_wait_limit(unsigned polls);
 
+/* Kernel-duration measurement for benchmarks.  Between
+ * lsk_dispatch_timing_begin and lsk_dispatch_timing_end on one host thread,
+ * each kernel the library launches from that thread (up to max_dispatches,
+ * 1..65536) carries a start/stop event pair bound to the dispatch itself, so
+ * the elapsed time is the kernel's own execution time, as a profiler's
+ * kernel trace measures it (no launch gaps).  end waits for those events,
+ * writes the duration in microseconds of the first min(capacity, n) timed
+ * dispatches, in launch order, to durations_us (host) and n to *dispatches
+ * (launches past max_dispatches run untimed).  Not for launches into a
+ * stream that is being captured.  No counterpart in the reference, whose
+ * benchmarks time with torch CUDA events around whole calls. */
+int lsk_dispatch_timing_begin(int max_dispatches);
+int lsk_dispatch_timing_end(float* durations_us, int capacity, int* dispatches);
+
 #ifdef __cplusplus
 }
 #endif

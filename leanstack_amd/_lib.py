@@ -118,6 +118,8 @@ _SIGNATURES.update({
     "lsk_stack_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
     "lsk_linear_error": (_c_int, [_c_void, ctypes.POINTER(_c_int)]),
     "lsk_set_linear_wait_limit": (None, [ctypes.c_uint]),
+    "lsk_dispatch_timing_begin": (_c_int, [_c_int]),
+    "lsk_dispatch_timing_end": (_c_int, [ctypes.POINTER(ctypes.c_float), _c_int, ctypes.POINTER(_c_int)]),
 })
 
 _lock = threading.Lock()

@@ -35,6 +35,42 @@ int hip_fail(hipError_t err, const char* what) {
 
 }  // namespace
 
+namespace lsk {
+namespace {
+
+// A dispatch timing of one host thread: two events per dispatch, handed out
+// in launch order by dispatch_timing_events.
+struct DispatchTiming {
+  std::vector<hipEvent_t> events;
+  int used = 0;
+  bool active = false;
+};
+
+DispatchTiming& dispatch_timing() {
+  thread_local DispatchTiming t;
+  return t;
+}
+
+void release_events(DispatchTiming& t) {
+  for (hipEvent_t e : t.events) (void)hipEventDestroy(e);
+  t.events.clear();
+  t.used = 0;
+  t.active = false;
+}
+
+}  // namespace
+
+bool dispatch_timing_events(hipEvent_t* start, hipEvent_t* stop) {
+  DispatchTiming& t = dispatch_timing();
+  if (!t.active || 2 * (size_t)(t.used + 1) > t.events.size()) return false;
+  *start = t.events[2 * t.used];
+  *stop = t.events[2 * t.used + 1];
+  ++t.used;
+  return true;
+}
+
+}  // namespace lsk
+
 // Synchronously read and clear word `index` of a workspace.
 int read_clear_error_word(void* workspace, int index, int* error_out) {
   if (workspace == nullptr || error_out == nullptr) return fail(LSK_ERR_INVALID, "null argument");
@@ -394,6 +430,48 @@ int lsk_stack_run(const void* program_dev, int count, void* workspace, size_t ws
 int lsk_stack_error(void* workspace, int* error_out) {
   lsk::clear_error();
   return read_clear_error_word(workspace, lsk::kStackWsError, error_out);
+}
+
+int lsk_dispatch_timing_begin(int max_dispatches) {
+  lsk::DispatchTiming& t = lsk::dispatch_timing();
+  if (t.active) return fail(LSK_ERR_INVALID, "a dispatch timing is already active on this thread");
+  if (max_dispatches < 1 || max_dispatches > 65536)
+    return fail(LSK_ERR_INVALID, "max_dispatches=%d outside 1..65536", max_dispatches);
+  t.events.reserve(2 * (size_t)max_dispatches);
+  for (int i = 0; i < 2 * max_dispatches; ++i) {
+    hipEvent_t e = nullptr;
+    const hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      lsk::release_events(t);
+      return hip_fail(err, "hipEventCreate");
+    }
+    t.events.push_back(e);
+  }
+  t.used = 0;
+  t.active = true;
+  return LSK_OK;
+}
+
+int lsk_dispatch_timing_end(float* durations_us, int capacity, int* dispatches) {
+  lsk::DispatchTiming& t = lsk::dispatch_timing();
+  if (!t.active) return fail(LSK_ERR_INVALID, "no dispatch timing is active on this thread");
+  if (dispatches == nullptr || capacity < 0 || (capacity > 0 && durations_us == nullptr)) {
+    lsk::release_events(t);
+    return fail(LSK_ERR_INVALID, "null or negative argument");
+  }
+  for (int i = 0; i < t.used; ++i) {
+    float ms = 0.f;
+    hipError_t err = hipEventSynchronize(t.events[2 * i + 1]);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, t.events[2 * i], t.events[2 * i + 1]);
+    if (err != hipSuccess) {
+      lsk::release_events(t);
+      return hip_fail(err, "dispatch timing events");
+    }
+    if (i < capacity) durations_us[i] = ms * 1e3f;
+  }
+  *dispatches = t.used;
+  lsk::release_events(t);
+  return LSK_OK;
 }
 
 int lsk_linear_error(void* workspace, int* error_out) {

@@ -475,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs arg
 
 template <int G, int NU, bool DYN = false>
 hipError_t launch_gu(const AttnArgs& a, hipStream_t stream) {
-  decode_attention_kernel<G, NU, DYN><<<dim3(a.n_kv * a.grid_chunks), dim3(kThreads), 0, stream>>>(a);
+  launch_kernel(decode_attention_kernel<G, NU, DYN>, dim3(a.n_kv * a.grid_chunks), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -739,7 +739,7 @@ hipError_t launch_decode_cfg(const DecodeArgs& a, hipStream_t stream) {
       if (raised != hipSuccess) return raised;
     }
   }
-  kernel<<<dim3(a.NB / RBW), dim3(NW * 64), lds, stream>>>(
+  launch_kernel(kernel, dim3(a.NB / RBW), dim3(NW * 64), lds, stream,
       static_cast<const bf16x8_t*>(a.w), static_cast<const __bf16*>(a.x), a.ldx, static_cast<__bf16*>(a.y), a.ldy,
       static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT, static_cast<const __bf16*>(a.norm_w), a.eps);
   return hipGetLastError();
@@ -848,7 +848,7 @@ hipError_t launch_half_cfg(const DecodeArgs& a, hipStream_t stream) {
   const size_t lds = NORM > 0    ? (size_t)NW * rms_wave_bytes(2 * U, NORM, a.M, RBW)
                      : NORM < -1 ? (size_t)NW * staged_wave_bytes(2 * U, a.M, RBW)
                                  : 0;
-  decode_half_kernel<NW, RBW, EPI, U, NORM><<<dim3(a.NB / RBW * 2), dim3(NW * 64), lds, stream>>>(
+  launch_kernel(decode_half_kernel<NW, RBW, EPI, U, NORM>, dim3(a.NB / RBW * 2), dim3(NW * 64), lds, stream,
       static_cast<const bf16x8_t*>(a.w), static_cast<const __bf16*>(a.x), a.ldx, static_cast<__bf16*>(a.y), a.ldy,
       static_cast<const __bf16*>(a.residual), a.ldr, a.M, a.KT, static_cast<const __bf16*>(a.norm_w), a.eps);
   return hipGetLastError();
@@ -1000,12 +1000,12 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
     constexpr int kNC = decltype(tag)::value;
     if (nw != nullptr) {
       const size_t lds = (size_t)kLmHeadWaves * rms_wave_bytes(10, kNC, M, kLmHeadRBW);
-      lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC, true><<<dim3(P), dim3(kLmHeadWaves * 64), lds, stream>>>(
+      launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC, true>, dim3(P), dim3(kLmHeadWaves * 64), lds, stream,
           static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
           KT, nw, eps);
     } else {
       const size_t lds = (size_t)kLmHeadWaves * staged_wave_bytes(10, M, kLmHeadRBW);
-      lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC><<<dim3(P), dim3(kLmHeadWaves * 64), lds, stream>>>(
+      launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC>, dim3(P), dim3(kLmHeadWaves * 64), lds, stream,
           static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
           KT, nullptr, 0.f);
     }
@@ -1033,17 +1033,17 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
   } else if (nw != nullptr) {
     return hipErrorInvalidValue;  // the fused RMSNorm serves K = 2560, M <= 8 (checked by the caller)
   } else if (KT == 80) {
-    lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
+    launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10>, dim3(P), dim3(kLmHeadWaves * 64), 0, stream,
         static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
         KT, nullptr, 0.f);
   } else {
-    lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 0><<<dim3(P), dim3(kLmHeadWaves * 64), 0, stream>>>(
+    launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 0>, dim3(P), dim3(kLmHeadWaves * 64), 0, stream,
         static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
         KT, nullptr, 0.f);
   }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  argmax_finalize_kernel<<<dim3(M), dim3(kFinalizeThreads), 0, stream>>>(partials, P, out_idx);
+  launch_kernel(argmax_finalize_kernel, dim3(M), dim3(kFinalizeThreads), 0, stream, partials, P, out_idx);
   return hipGetLastError();
 }
 

@@ -461,7 +461,7 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
                   const void* residual, int ldr, hipStream_t stream) {
   const int n_blocks = N / BN;
   const int m_blocks = (M + BM - 1) / BM;
-  gemm256_kernel<EPI><<<dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream>>>(
+  launch_kernel(gemm256_kernel<EPI>, dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream,
       static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
       static_cast<const __bf16*>(residual), ldr, M, K / kTileK, n_blocks, m_blocks);
   return hipGetLastError();
@@ -1208,7 +1208,7 @@ hipError_t launch(const void* w, int N, int K, const void* x, int M, int ldx, vo
   k.partials = ws != nullptr ? ws + kSkPartialsOffset : nullptr;
   k.partial_bytes = (unsigned)((size_t)k.R * k.S * kSkPartialBytes);
   k.spin_limit = g_wait_limit.load(std::memory_order_relaxed);
-  gemm_wdx_kernel<EPI, A, TB><<<dim3(k.dp + k.R * k.S), dim3(kThreads), 0, stream>>>(g, k);
+  launch_kernel(gemm_wdx_kernel<EPI, A, TB>, dim3(k.dp + k.R * k.S), dim3(kThreads), 0, stream, g, k);
   return hipGetLastError();
 }
 
@@ -1219,7 +1219,7 @@ hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx
                       const void* residual, int ldr, hipStream_t stream) {
   const int n_blocks = N / kGemmBN;
   const int m_blocks = (M + kGemmBM - 1) / kGemmBM;
-  gemm_linear_kernel<EPI><<<dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream>>>(
+  launch_kernel(gemm_linear_kernel<EPI>, dim3(n_blocks * m_blocks), dim3(kThreads), 0, stream,
       static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, static_cast<__bf16*>(y), ldy,
       static_cast<const __bf16*>(residual), ldr, M, K / kTileK, n_blocks, m_blocks);
   return hipGetLastError();

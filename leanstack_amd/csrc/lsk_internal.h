@@ -2,6 +2,7 @@
 // kernel translation units (decode.hip, gemm.hip).  Not part of the ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -163,6 +164,26 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
 
 // Records a HIP failure for lsk_last_error (defined in abi.cpp).
 int fail_hip_call(hipError_t err, const char* what);
+
+// The next start/stop event pair of a dispatch timing active on this host
+// thread (lsk_dispatch_timing_begin), or false when none is active or its
+// pairs are used up (defined in abi.cpp).
+bool dispatch_timing_events(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel the library launches goes through here: with a dispatch
+// timing active, the event pair is bound to the dispatch itself
+// (hipExtLaunchKernelGGL), so its elapsed time is the kernel's own duration.
+template <typename... KArgs, typename... Args>
+inline void launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                          Args... args) {
+  static_assert(sizeof...(KArgs) == sizeof...(Args), "one argument per kernel parameter");
+  hipEvent_t start, stop;
+  if (dispatch_timing_events(&start, &stop))
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, stream, start, stop, 0u,
+                          static_cast<KArgs>(args)...);
+  else
+    kernel<<<grid, block, lds, stream>>>(static_cast<KArgs>(args)...);
+}
 
 // Workspace bytes the split-K prefill path needs on `device` for this shape
 // (0 when the shape does not take it).  Sets *status to a HIP error if the

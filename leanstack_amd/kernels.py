@@ -109,6 +109,25 @@ def set_linear_wait_limit(polls: int) -> None:
 LINEAR_WAIT_LIMIT_DEFAULT = 1 << 22
 
 
+def kernel_durations_us(fn, max_dispatches: int = 4096) -> list[float]:
+    """Run fn() (eager launches of this library's kernels on the current
+    stream) with every dispatch timed by events bound to the dispatch itself
+    (lsk_dispatch_timing_begin/end), and return each kernel's own duration in
+    microseconds, in launch order.  Waits for the timed kernels."""
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("dispatch timing cannot run inside a graph capture")
+    lib = _lib.load()
+    _lib.check(lib.lsk_dispatch_timing_begin(int(max_dispatches)), "lsk_dispatch_timing_begin")
+    durations = (ctypes.c_float * int(max_dispatches))()
+    count = ctypes.c_int(0)
+    try:
+        fn()
+    finally:
+        status = lib.lsk_dispatch_timing_end(durations, int(max_dispatches), ctypes.byref(count))
+    _lib.check(status, "lsk_dispatch_timing_end")
+    return [float(durations[i]) for i in range(min(count.value, int(max_dispatches)))]
+
+
 def linear_error(workspace: torch.Tensor) -> int:
     """Read and clear the error word of a prefill workspace (0 = no bounded
     wait gave up since the last read).  Synchronous."""

@@ -60,6 +60,30 @@ def test_reference_hot_kernel_cases(gpu, case):
     assert_parity(_gpu_linear(x, w), ref.linear(x, w), case)
 
 
+def test_dispatch_timing_times_each_kernel(gpu):
+    """lsk_dispatch_timing_begin/end bind an event pair to each dispatch:
+    one positive duration per kernel launched, in order, results unchanged;
+    launches past the limit run untimed; no nested or unmatched timing."""
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(weight(2560, 4096, seed=3).to(dev))
+    xd = activations(1, 4096, seed=4).to(dev)
+    plain = kernels.linear(xd, pw)
+    torch.cuda.synchronize()
+    outs = []
+    durs = kernels.kernel_durations_us(lambda: outs.extend(kernels.linear(xd, pw) for _ in range(5)), max_dispatches=8)
+    assert len(durs) == 5 and all(0.0 < d < 1e4 for d in durs), durs
+    for o in outs:
+        assert torch.equal(o.view(torch.int16), plain.view(torch.int16))
+    assert len(kernels.kernel_durations_us(lambda: [kernels.linear(xd, pw) for _ in range(3)], max_dispatches=2)) == 2
+    lib = _lib.load()
+    n = ctypes.c_int(-1)
+    assert lib.lsk_dispatch_timing_begin(4) == _lib.OK
+    assert lib.lsk_dispatch_timing_begin(4) == _lib.ERR_INVALID
+    assert lib.lsk_dispatch_timing_end(None, 0, ctypes.byref(n)) == _lib.OK and n.value == 0
+    assert lib.lsk_dispatch_timing_end(None, 0, ctypes.byref(n)) == _lib.ERR_INVALID
+    assert lib.lsk_dispatch_timing_begin(0) == _lib.ERR_INVALID
+
+
 def test_auto_workspaces_are_per_stream(gpu):
     """workspace="auto" keeps one split-K workspace per (device, stream):
     calls on another stream never share the arrival flags and partial slots
