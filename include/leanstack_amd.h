@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 2
+#define LSK_ABI_VERSION 3
 
 enum lsk_layout {
   LSK_LAYOUT_ROWMAJOR = 0,        /* plain W[N][K]; accepted by the packer only */
@@ -224,7 +224,16 @@ int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_di
  *                (src/leanstack/runtime/qwen_explicit.py:952-960).
  *   logits_opt   NULL, or device fp32 [M][V] that receives the scores.
  *   out_idx      device int64 [M].
- *   workspace    lsk_workspace_bytes(LSK_OP_LM_HEAD_ARGMAX, M, V, K) bytes.
+ *   workspace    lsk_workspace_bytes(LSK_OP_LM_HEAD_ARGMAX, M, V, K) bytes,
+ *                8-byte aligned, ZERO-FILLED before its first use (e.g.
+ *                hipMemset(ws, 0, bytes)); every call leaves it zero again,
+ *                so one zeroing serves every later call.  Calls that share a
+ *                workspace must be stream-ordered.  Its first word counts
+ *                argmax stages that gave up waiting for a partial (then
+ *                that row's out_idx is -1); it stays 0 while the grid runs
+ *                to completion.
+ * One launch: the workgroups store per-tile maxima and the last M
+ * workgroups of the grid reduce them.
  * Replaces cutile_logits_argmax (src/leanstack/runtime/cutile_logits.py:37-69)
  * and the per-position head loop of the verify path
  * (experiments/models/qwen_explicit_runtime_loop.py:805-812) with one M-row
@@ -241,20 +250,21 @@ int lsk_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K,
  * be 2560 (the Qwen3-4B hidden size) and M at most 8.  Replaces the final
  * norm and head of src/leanstack/runtime/qwen_explicit.py:952-960 (and,
  * with LSK_LOGITS_FP32, the norm in front of cutile_logits_argmax,
- * qwen_explicit.py:1807-1832) in one launch plus the argmax stage. */
+ * qwen_explicit.py:1807-1832) in the same one launch. */
 int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, int K,
                                     const void* x, int M, int ldx,
                                     const void* norm_weight, float eps,
                                     float* logits_opt, int logits_mode, long long* out_idx,
                                     void* workspace, size_t ws_bytes, void* hip_stream);
 
-/* lsk_lm_head_argmax_bf16 without the workspace: the argmax partials live in
- * a static device array of the library (1 MiB per device), so the call
- * allocates nothing.  No counterpart in the reference; it is for callers that
- * cannot allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc).  Limit: M * (V / 32) * 8 bytes of
- * partials must fit in 1 MiB (every M <= 16 at V = 151936); larger calls
- * return LSK_ERR_INVALID before anything touches the GPU.  All calls on one
+/* lsk_lm_head_argmax_bf16 without the workspace: the argmax workspace lives
+ * in a static device array of the library (1 MiB per device, zero from load
+ * time), so the call allocates nothing.  No counterpart in the reference; it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Limit:
+ * 64 + M * (V / 32) * 8 bytes must fit in 1 MiB (every M <= 16 at
+ * V = 151936); larger calls return LSK_ERR_INVALID before anything touches
+ * the GPU.  All calls on one
  * device share the array: calls that overlap in time on a device (streams not
  * ordered with each other) race; stream-ordered calls do not. */
 int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_id, int V, int K,

@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must be loaded first: the library shares its HIP ru
 LIBRARY_PATH = Path(__file__).resolve().parent / "libleanstack_amd.so"
 HEADER_PATH = Path(__file__).resolve().parent.parent / "include" / "leanstack_amd.h"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # enum lsk_layout / lsk_epilogue / lsk_op / lsk_logits_mode / lsk_status
 LAYOUT_ROWMAJOR = 0

@@ -100,7 +100,7 @@ size_t lsk_workspace_bytes(int op, int M, int N, int K) {
   }
   if (op == LSK_OP_LM_HEAD_ARGMAX) {
     if (M < 1 || M > lsk::kDecodeMaxM || N <= 0 || K <= 0 || N % (2 * lsk::kTileRows) != 0) return 0;
-    return (size_t)M * (size_t)lsk::lm_head_partials(N) * sizeof(lsk::ArgmaxPartial);
+    return lsk::lm_head_workspace_bytes(M, N);
   }
   return 0;
 }
@@ -256,7 +256,7 @@ int lm_head_argmax(const void* w_packed, int layout_id, int V, int K, const void
   if (workspace == nullptr || ws_bytes < need || !aligned(workspace, 8))
     return fail(LSK_ERR_WORKSPACE, "lm_head workspace needs %zu bytes, got %zu", need, workspace ? ws_bytes : 0);
   hipError_t err = lsk::launch_lm_head_argmax(w_packed, V, K, x, M, ldx, logits_opt, logits_mode == LSK_LOGITS_BF16,
-                                              out_idx, static_cast<lsk::ArgmaxPartial*>(workspace), norm_weight, eps,
+                                              out_idx, workspace, norm_weight, eps,
                                               static_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess) return hip_fail(err, "lm_head kernel launch");
   return LSK_OK;

@@ -574,16 +574,119 @@ __device__ __forceinline__ void argmax_take(float& best, int& best_idx, float s,
   }
 }
 
-// lm_head scores for RBW row-blocks (vocab rows) + the workgroup's argmax.
-// Grid: (NB / RBW) workgroups; partial[m * P + blockIdx.x] = best (score, index).
+typedef __attribute__((address_space(1))) unsigned long long global_u64_t;
+
+// The argmax partials live in the workspace as 64-bit words: the score's bits
+// in the low half and index + 1 in the high half, so a word that is zero has
+// not been written by this call yet (between calls every word is zero).
+// Stores and loads are device-coherent: partials cross XCDs.
+__device__ __forceinline__ void store_partial(ArgmaxPartial* p, float score, int index) {
+  const unsigned long long v =
+      (unsigned long long)__builtin_bit_cast(unsigned, score) | ((unsigned long long)(unsigned)(index + 1) << 32);
+  __hip_atomic_store((global_u64_t*)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long load_partial(const ArgmaxPartial* p) {
+  return __hip_atomic_load((const global_u64_t*)(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr unsigned kHeadSpinLimit = 1u << 20;  // polls of one partial before the second stage gives up
+#ifndef LSK_LMHEAD_ROUND
+#define LSK_LMHEAD_ROUND 10
+#endif
+constexpr int kRoundLoads = LSK_LMHEAD_ROUND;                 // partial loads in flight per thread of the second stage
+
+// Second stage of the greedy head, as the host-side torch.argmax over tile
+// maxima in src/leanstack/runtime/cutile_logits.py:67-69: the NT threads of
+// one workgroup reduce the P partials of one activation row into *out, then
+// zero them for the next call.  Every load of a round is issued before the
+// first compare; a partial still zero (its workgroup has not stored it) is
+// polled again.  argmax_take is a total order on (score, index), so the
+// result does not depend on the order partials are combined in.  A partial
+// that stays zero for kHeadSpinLimit polls makes the row's result -1 and
+// counts one give-up in *status (neither happens while every workgroup of
+// the grid runs to its end, which nothing in the grid waits on).
+template <int NT>
+__device__ __forceinline__ void reduce_row_partials(ArgmaxPartial* __restrict__ row, int P,
+                                                    long long* __restrict__ out, unsigned* __restrict__ status) {
+  constexpr int kW = NT / 64;
+  __shared__ float s_best[kW];
+  __shared__ int s_idx[kW];
+  __shared__ int s_gave_up[kW];
+  const int t = (int)threadIdx.x;
+  float best = -__builtin_huge_valf();
+  int best_idx = INT_MAX;
+  bool gave_up = false;
+  for (int base = 0; base < P; base += NT * kRoundLoads) {
+    unsigned long long v[kRoundLoads];
+#pragma unroll
+    for (int j = 0; j < kRoundLoads; ++j) {
+      const int p = base + j * NT + t;
+      v[j] = p < P ? load_partial(row + p) : 0ull;
+    }
+#pragma unroll
+    for (int j = 0; j < kRoundLoads; ++j) {
+      const int p = base + j * NT + t;
+      if (p >= P) continue;
+      for (unsigned spins = 0; (v[j] >> 32) == 0;) {
+        if (++spins > kHeadSpinLimit) {
+          gave_up = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        v[j] = load_partial(row + p);
+      }
+      __hip_atomic_store((global_u64_t*)(row + p), 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((v[j] >> 32) != 0)
+        argmax_take(best, best_idx, __builtin_bit_cast(float, (unsigned)v[j]), (int)(v[j] >> 32) - 1);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float os = __shfl_xor(best, off);
+    const int oi = __shfl_xor(best_idx, off);
+    argmax_take(best, best_idx, os, oi);
+  }
+  const bool wave_gave_up = __any(gave_up);
+  if ((t & 63) == 0) {
+    s_best[t >> 6] = best;
+    s_idx[t >> 6] = best_idx;
+    s_gave_up[t >> 6] = wave_gave_up;
+  }
+  __syncthreads();
+  if (t == 0) {
+    bool any_gave_up = false;
+    for (int w = 0; w < kW; ++w) {
+      argmax_take(best, best_idx, s_best[w], s_idx[w]);
+      any_gave_up |= s_gave_up[w] != 0;
+    }
+    *out = any_gave_up ? -1 : best_idx;
+    if (any_gave_up) __hip_atomic_fetch_add(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// lm_head scores for RBW row-blocks (vocab rows) + the argmax, in one launch.
+// Grid: P = NB / RBW scoring workgroups, then M reducing ones.  Scoring
+// workgroup b stores partial[m * P + b] = its best (score, index) for row m;
+// reducing workgroup P + m -- dispatched after every scoring one, so it waits
+// only for workgroups that are running or done -- reduces row m into
+// out_idx[m] while the last scoring workgroups finish (reduce_row_partials).
+// The workspace must be zero when a call starts, and every call leaves it
+// zero.
 // NC > 0: the activations staged through LDS (NC chunks per lane), or with
 // NORM their RMSNorm (norm_w, eps) applied on the way (the dense prologue).
 template <int NW, int RBW, int U, int NC = 0, bool NORM = false>
 __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, float* __restrict__ logits,
-    int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, int M, int KT,
-    const __bf16* __restrict__ norm_w, float eps) {
+    int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, unsigned* __restrict__ status,
+    long long* __restrict__ out_idx, int M, int KT, const __bf16* __restrict__ norm_w, float eps) {
   static_assert(!NORM || NC > 0, "the RMSNorm prologue is the dense single-round one");
+  const int P = (int)gridDim.x - M;
+  if ((int)blockIdx.x >= P) {
+    const int row = (int)blockIdx.x - P;
+    reduce_row_partials<NW * 64>(partial + (size_t)row * P, P, out_idx + row, status);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m = lane & 15;
@@ -598,100 +701,60 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
   for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
+  bool leader;  // wave 0, which holds the sums after reduce_waves
   if constexpr (NORM) {
     (void)xrow;
     (void)ke;
     accumulate_rows_rms_dense<NW, RBW, U, NC>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w), M, KT,
                                               kb, wave, lane, eps);
-    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NC, M, RBW))) return;
+    leader = reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NC, M, RBW));
   } else if constexpr (NC > 0) {  // activations staged through LDS, NC chunks per lane
     (void)xrow;
     (void)ke;
     (void)norm_w;
     (void)eps;
     accumulate_rows_staged<NW, RBW, U, NC, false>(acc, wt, x, ldx, M, KT, kb, wave, lane);
-    if (!reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RBW))) return;
+    leader = reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RBW));
   } else {
     (void)norm_w;
     (void)eps;
     accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
-    if (!reduce_waves<NW, RBW>(acc, wave, lane)) return;
+    leader = reduce_waves<NW, RBW>(acc, wave, lane);
   }
 
-  // Scan this lane's rows in increasing index order with the torch.argmax
-  // order (argmax_beats): every row, -inf and NaN included, gets a real index.
-  float best = -__builtin_huge_valf();
-  int best_idx = INT_MAX;
+  if (leader) {
+    // Scan this lane's rows in increasing index order with the torch.argmax
+    // order (argmax_beats): every row, -inf and NaN included, gets a real index.
+    float best = -__builtin_huge_valf();
+    int best_idx = INT_MAX;
 #pragma unroll
-  for (int r = 0; r < RBW; ++r) {
-    const int n0 = (rb0 + r) * 16 + 4 * g;
-    f32x4_t s = acc[r];
-    if (logits_bf16) {
+    for (int r = 0; r < RBW; ++r) {
+      const int n0 = (rb0 + r) * 16 + 4 * g;
+      f32x4_t s = acc[r];
+      if (logits_bf16) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[i] = bf16_round(s[i]);
+        for (int i = 0; i < 4; ++i) s[i] = bf16_round(s[i]);
+      }
+      if (logits != nullptr && m_active) *reinterpret_cast<f32x4_t*>(logits + (size_t)m * V + n0) = s;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) argmax_take(best, best_idx, s[i], n0 + i);
     }
-    if (logits != nullptr && m_active) *reinterpret_cast<f32x4_t*>(logits + (size_t)m * V + n0) = s;
+    // Lanes m, m+16, m+32, m+48 hold the same column: combine them.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) argmax_take(best, best_idx, s[i], n0 + i);
-  }
-  // Lanes m, m+16, m+32, m+48 hold the same column: combine them.
-#pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    const float os = __shfl_xor(best, off);
-    const int oi = __shfl_xor(best_idx, off);
-    argmax_take(best, best_idx, os, oi);
-  }
-  if (g == 0 && m_active) partial[(size_t)m * gridDim.x + blockIdx.x] = ArgmaxPartial{best, best_idx};
-}
-
-// Second stage: one workgroup per activation row reduces the P partials,
-// as the host-side torch.argmax over tile maxima does in
-// src/leanstack/runtime/cutile_logits.py:67-69.  Each thread issues all of
-// its partial loads before comparing, so the stage costs about one memory
-// latency.
-constexpr int kFinalizeThreads = 1024;
-constexpr int kFinalizePerThread = 8;
-
-
-__global__ __launch_bounds__(kFinalizeThreads) void argmax_finalize_kernel(const ArgmaxPartial* __restrict__ partial,
-                                                                           int P, long long* __restrict__ out_idx) {
-  const int m = blockIdx.x;
-  const ArgmaxPartial* row = partial + (size_t)m * P;
-  float best = -__builtin_huge_valf();
-  int best_idx = INT_MAX;
-  for (int base = 0; base < P; base += kFinalizeThreads * kFinalizePerThread) {
-    ArgmaxPartial c[kFinalizePerThread];
-#pragma unroll
-    for (int j = 0; j < kFinalizePerThread; ++j) {
-      const int p = base + j * kFinalizeThreads + (int)threadIdx.x;
-      c[j] = p < P ? row[p] : ArgmaxPartial{-__builtin_huge_valf(), INT_MAX};
+    for (int off = 16; off <= 32; off <<= 1) {
+      const float os = __shfl_xor(best, off);
+      const int oi = __shfl_xor(best_idx, off);
+      argmax_take(best, best_idx, os, oi);
     }
-#pragma unroll
-    for (int j = 0; j < kFinalizePerThread; ++j) argmax_take(best, best_idx, c[j].score, c[j].index);
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float os = __shfl_xor(best, off);
-    const int oi = __shfl_xor(best_idx, off);
-    argmax_take(best, best_idx, os, oi);
-  }
-  constexpr int kW = kFinalizeThreads / 64;
-  __shared__ float s_best[kW];
-  __shared__ int s_idx[kW];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    s_best[wave] = best;
-    s_idx[wave] = best_idx;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kW; ++w) argmax_take(best, best_idx, s_best[w], s_idx[w]);
-    out_idx[m] = best_idx;
+    if (g == 0 && m_active) store_partial(partial + (size_t)m * P + blockIdx.x, best, best_idx);
   }
 }
 
 constexpr int kLmHeadWaves = 8;
-constexpr int kLmHeadRBW = 2;
+#ifndef LSK_LMHEAD_RBW
+#define LSK_LMHEAD_RBW 2
+#endif
+constexpr int kLmHeadRBW = LSK_LMHEAD_RBW;
 
 // Launch arguments of one decode / verify projection.
 struct DecodeArgs {
@@ -990,30 +1053,35 @@ hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void*
 int lm_head_partials(int V) { return (V / kTileRows) / kLmHeadRBW; }
 
 hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int M, int ldx, float* logits,
-                                 int logits_bf16, long long* out_idx, ArgmaxPartial* partials,
+                                 int logits_bf16, long long* out_idx, void* workspace,
                                  const void* norm_w, float eps, hipStream_t stream) {
   const int NB = V / kTileRows;
   const int KT = K / kTileK;
   const int P = NB / kLmHeadRBW;
+  auto* status = static_cast<unsigned*>(workspace);
+  auto* partials = reinterpret_cast<ArgmaxPartial*>(static_cast<unsigned char*>(workspace) + kLmHeadStatusBytes);
   const auto* nw = static_cast<const __bf16*>(norm_w);
   auto staged = [&](auto tag) {
     constexpr int kNC = decltype(tag)::value;
     if (nw != nullptr) {
       const size_t lds = (size_t)kLmHeadWaves * rms_wave_bytes(10, kNC, M, kLmHeadRBW);
-      launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC, true>, dim3(P), dim3(kLmHeadWaves * 64), lds, stream,
-          static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+      launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC, true>, dim3(P + M), dim3(kLmHeadWaves * 64), lds, stream,
+          static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, status, out_idx, M,
           KT, nw, eps);
     } else {
       const size_t lds = (size_t)kLmHeadWaves * staged_wave_bytes(10, M, kLmHeadRBW);
-      launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC>, dim3(P), dim3(kLmHeadWaves * 64), lds, stream,
-          static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+      launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10, kNC>, dim3(P + M), dim3(kLmHeadWaves * 64), lds, stream,
+          static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, status, out_idx, M,
           KT, nullptr, 0.f);
     }
   };
   // K/32 = 80: 8 waves x 10 k-tiles; for M <= 8 the activations are staged
   // through LDS (the wave's 40 M chunks over 64 lanes).
   if (KT == 80 && M <= 8) {
-    switch ((40 * M + 63) / 64) {
+#ifndef LSK_LMHEAD_NC_MIN
+#define LSK_LMHEAD_NC_MIN 1
+#endif
+    switch (std::max((40 * M + 63) / 64, LSK_LMHEAD_NC_MIN)) {
       case 1:
         staged(std::integral_constant<int, 1>{});
         break;
@@ -1033,17 +1101,14 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
   } else if (nw != nullptr) {
     return hipErrorInvalidValue;  // the fused RMSNorm serves K = 2560, M <= 8 (checked by the caller)
   } else if (KT == 80) {
-    launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10>, dim3(P), dim3(kLmHeadWaves * 64), 0, stream,
-        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+    launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 10>, dim3(P + M), dim3(kLmHeadWaves * 64), 0, stream,
+        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, status, out_idx, M,
         KT, nullptr, 0.f);
   } else {
-    launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 0>, dim3(P), dim3(kLmHeadWaves * 64), 0, stream,
-        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, M,
+    launch_kernel(lm_head_kernel<kLmHeadWaves, kLmHeadRBW, 0>, dim3(P + M), dim3(kLmHeadWaves * 64), 0, stream,
+        static_cast<const bf16x8_t*>(w), static_cast<const __bf16*>(x), ldx, logits, V, logits_bf16, partials, status, out_idx, M,
         KT, nullptr, 0.f);
   }
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  launch_kernel(argmax_finalize_kernel, dim3(M), dim3(kFinalizeThreads), 0, stream, partials, P, out_idx);
   return hipGetLastError();
 }
 

@@ -158,9 +158,18 @@ hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const 
 // Number of workgroups (= argmax partials per row) the lm_head kernel uses.
 int lm_head_partials(int V);
 
+// The lm_head workspace: a status header (word 0 counts second stages that
+// gave up waiting for a partial) followed by M * lm_head_partials(V) 64-bit
+// partials.  It must be zero when first used; every call leaves the partials
+// zero again.
+constexpr size_t kLmHeadStatusBytes = 64;
+inline size_t lm_head_workspace_bytes(int M, int V) {
+  return kLmHeadStatusBytes + (size_t)M * (size_t)lm_head_partials(V) * sizeof(ArgmaxPartial);
+}
+
 hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int M, int ldx,
                                  float* logits, int logits_bf16, long long* out_idx,
-                                 ArgmaxPartial* partials, const void* norm_w, float eps, hipStream_t stream);
+                                 void* workspace, const void* norm_w, float eps, hipStream_t stream);
 
 // Records a HIP failure for lsk_last_error (defined in abi.cpp).
 int fail_hip_call(hipError_t err, const char* what);

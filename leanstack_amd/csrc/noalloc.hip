@@ -1,18 +1,18 @@
 // Allocation-free greedy lm_head: lsk_lm_head_argmax_noalloc_bf16.
 //
-// The same two kernels as lsk_lm_head_argmax_bf16 (lm_head_kernel writes one
-// (score, index) partial per workgroup and activation row, argmax_finalize
-// reduces them), with the partials in `scratch`, a file-scope device array,
-// instead of a caller-allocated workspace.  For callers that cannot allocate
-// device memory: code under HIP graph capture, tight serving loops.
+// The same kernel as lsk_lm_head_argmax_bf16 (lm_head_kernel writes one
+// (score, index) partial per workgroup and activation row, and its last M
+// workgroups reduce them), with its workspace in `scratch`, a file-scope
+// device array, instead of a caller-allocated one.  For callers that cannot
+// allocate device memory: code under HIP graph capture, tight serving loops.
 //
-// Limits and sharing: the partials of one call take M * (V / 32) * 8 bytes,
-// at most kScratchBytes (1 MiB: every M <= 16 at V = 151936, or M = 16 up to
-// V = 262144); larger calls are rejected before anything touches the GPU.
-// Every call on a device uses that device's one copy of the array, and each
-// call overwrites every partial it reads, so nothing needs clearing between
-// calls -- but calls that overlap in time on one device (unordered streams)
-// race on it.
+// Limits and sharing: one call's workspace takes 64 + M * (V / 32) * 8
+// bytes, at most kScratchBytes (1 MiB: every M <= 16 at V = 151936); larger
+// calls are rejected before anything touches the GPU.  The array starts
+// zeroed (a device global without an initializer) and every call leaves its
+// partials zero again, which is the state the kernel needs, so nothing is
+// cleared between calls -- but calls that overlap in time on one device
+// (unordered streams) race on it.
 
 #include <hip/hip_runtime.h>
 
@@ -57,20 +57,20 @@ extern "C" int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_
                                                long long* out_idx, void* hip_stream) {
   if (int st = lsk::check_lm_head_call(w_packed, layout_id, V, K, x, M, ldx, logits_opt, logits_mode, out_idx))
     return st;
-  const size_t need = (size_t)M * (size_t)lsk::lm_head_partials(V) * sizeof(lsk::ArgmaxPartial);
+  const size_t need = lsk::lm_head_workspace_bytes(M, V);
   if (need > kScratchBytes) {
     return lsk::fail(LSK_ERR_INVALID,
-                     "M=%d rows over V=%d need %zu bytes of argmax partials; the static scratch holds %zu "
-                     "(M * V / 32 * 8 bytes at most): use lsk_lm_head_argmax_bf16 with a workspace",
+                     "M=%d rows over V=%d need %zu bytes of argmax workspace; the static scratch holds %zu "
+                     "(64 + M * V / 32 * 8 bytes at most): use lsk_lm_head_argmax_bf16 with a workspace",
                      M, V, need, kScratchBytes);
   }
   int device = 0;
   hipError_t err = hipGetDevice(&device);
   if (err != hipSuccess) return lsk::fail_hip_call(err, "hipGetDevice");
-  void* partials = nullptr;
-  if (int st = scratch_address(device, &partials)) return st;
+  void* workspace = nullptr;
+  if (int st = scratch_address(device, &workspace)) return st;
   err = lsk::launch_lm_head_argmax(w_packed, V, K, x, M, ldx, logits_opt, logits_mode == LSK_LOGITS_BF16, out_idx,
-                                   static_cast<lsk::ArgmaxPartial*>(partials), nullptr, 0.f,
+                                   workspace, nullptr, 0.f,
                                    static_cast<hipStream_t>(hip_stream));
   if (err != hipSuccess) return lsk::fail_hip_call(err, "lm_head kernel launch");
   return LSK_OK;

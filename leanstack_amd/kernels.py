@@ -324,14 +324,23 @@ def decode_attention(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weig
 
 
 class LmHeadWorkspace:
-    """Device workspace of the two-stage argmax, sized once per (M, V, K)."""
+    """Device workspace of the greedy head, sized once per (M, V, K): a status
+    word and the per-workgroup argmax partials.  Zero-filled here; every call
+    leaves the partials zero again, so it is never cleared between calls.
+    Calls that share one must be stream-ordered."""
 
     def __init__(self, m: int, v: int, k: int, device: torch.device | str) -> None:
         nbytes = _lib.load().lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, m, v, k)
         if nbytes == 0:
             raise ValueError(f"no lm_head workspace for M={m}, V={v}, K={k}")
         self.m, self.v, self.k = m, v, k
-        self.buffer = torch.empty(nbytes, device=device, dtype=torch.uint8)
+        self.buffer = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+
+    def give_ups(self) -> int:
+        """Argmax stages (rows) that gave up waiting for a partial since the
+        workspace was made (their out_idx was -1); 0 while every grid runs to
+        its end.  Synchronizes with the device."""
+        return int(self.buffer[:4].view(torch.int32).item())
 
 
 def lm_head_argmax(hidden: torch.Tensor, weight: PackedWeight, *, logits_mode: int = _lib.LOGITS_FP32,

@@ -252,6 +252,10 @@ class ResidentArena:
         self.buffer = raw[skew : skew + plan.arena_bytes]
         self._index = {e.name: e for e in plan.entries}
         self.load_stats: dict[str, int] | None = None  # set by the pack loader
+        if "scratch.argmax_workspace" in self._index:
+            # the greedy head's workspace must start zeroed (each call leaves
+            # it so)
+            self.view("scratch.argmax_workspace").zero_()
 
     def weight_names(self) -> set[str]:
         """Entries a pack must fill: everything but scratch and the KV cache."""

@@ -154,7 +154,7 @@ def test_lm_head_rejects_before_launch():
     lib = _lib.load()
     ok = dict(V=151936, K=2560, M=1)
     ws = lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 1, 151936, 2560)
-    assert ws == (151936 // 32) * 8
+    assert ws == 64 + (151936 // 32) * 8  # status header + one partial per 32 vocab rows
     cases = [
         (dict(M=17), _lib.ERR_INVALID),
         (dict(V=151920), _lib.ERR_INVALID),   # V % 32 != 0
@@ -279,8 +279,8 @@ def test_launch_next_refuses_a_bad_token_buffer():
 
 
 def test_noalloc_lm_head_rejects_before_launch():
-    """The allocation-free head refuses calls whose partials exceed its
-    static scratch (M * V / 32 * 8 bytes > 1 MiB) and the usual bad
+    """The allocation-free head refuses calls whose workspace exceeds its
+    static scratch (64 + M * V / 32 * 8 bytes > 1 MiB) and the usual bad
     arguments, before touching the GPU."""
     lib = _lib.load()
 
@@ -291,6 +291,8 @@ def test_noalloc_lm_head_rejects_before_launch():
                                                    a["logits"], a["mode"], a["out"], None)
 
     st = call(m=16, v=1 << 19)  # 16 rows x 16384 partials x 8 B = 2 MiB
+    assert st == _lib.ERR_INVALID and "static scratch" in _lib.last_error()
+    st = call(m=16, v=1 << 18)  # partials fill exactly 1 MiB: the status header is 64 bytes over
     assert st == _lib.ERR_INVALID and "static scratch" in _lib.last_error()
     assert call(m=17) == _lib.ERR_INVALID
     assert call(layout=2) == _lib.ERR_LAYOUT

@@ -355,6 +355,41 @@ def test_lm_head_argmax_bf16_mode(gpu):
     assert torch.equal(idx, expect)
 
 
+def test_lm_head_workspace_left_zero_across_calls(gpu):
+    """One workspace through calls of M = 16, 1, 8, 3, 16 in a row, eager and
+    replayed from a graph: each call's argmax meets the oracle, and after each
+    call the whole workspace (status word and every partial) is zero again,
+    which is the state the next call starts from."""
+    e = weight(G.vocab_size, G.hidden_size, seed=73)
+    dev = torch.device("cuda:0")
+    pw = PackedWeight.from_rowmajor(e.to(dev))
+    ws = kernels.LmHeadWorkspace(16, G.vocab_size, G.hidden_size, dev)
+    for i, m in enumerate((16, 1, 8, 3, 16)):
+        h = activations(m, G.hidden_size, seed=730 + i)
+        logits = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
+        idx = kernels.lm_head_argmax(h.to(dev), pw, logits_out=logits, workspace=ws).cpu()
+        assert_greedy_rows(idx, ref.logits_scores_fp32(h, e), logits.cpu(), f"call {i} M={m}")
+        assert int(torch.count_nonzero(ws.buffer)) == 0, f"workspace not zero after call {i} (M={m})"
+    # replays of one captured call with new inputs copied in between
+    m = 4
+    h_dev = torch.empty((m, G.hidden_size), device=dev, dtype=torch.bfloat16)
+    out = torch.empty((m,), device=dev, dtype=torch.long)
+    logits = torch.empty((m, G.vocab_size), device=dev, dtype=torch.float32)
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        kernels.lm_head_argmax(h_dev, pw, workspace=ws, out=out, logits_out=logits)
+    for i in range(3):
+        h = activations(m, G.hidden_size, seed=740 + i)
+        h_dev.copy_(h.to(dev))
+        out.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_greedy_rows(out.cpu(), ref.logits_scores_fp32(h, e), logits.cpu(), f"replay {i}")
+        assert int(torch.count_nonzero(ws.buffer)) == 0, f"workspace not zero after replay {i}"
+    assert ws.give_ups() == 0
+
+
 def test_lm_head_ties_pick_lowest_index(gpu):
     """Two identical maximal vocab rows: the lower index wins, in both modes."""
     v, k = 4096, 256

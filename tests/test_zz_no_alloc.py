@@ -24,7 +24,7 @@ def _both(e: PackedWeight, h: torch.Tensor, mode: int):
     lib = _lib.load()
     m, v, k = h.shape[0], e.n, e.k
     stream = kernels.stream_handle()
-    ws = torch.empty(lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, m, v, k), dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, m, v, k), dtype=torch.uint8, device=DEV)
     idx_ws = torch.full((m,), -1, dtype=torch.long, device=DEV)
     scores_ws = torch.empty((m, v), dtype=torch.float32, device=DEV)
     _lib.check(lib.lsk_lm_head_argmax_bf16(e.data.data_ptr(), e.layout, v, k, h.data_ptr(), m, k,
