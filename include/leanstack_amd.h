@@ -103,16 +103,24 @@ int lsk_pack_bf16(const void* w_rowmajor_host, int N, int K, int layout_id, void
 int lsk_unpack_bf16(const void* packed_host, int N, int K, int layout_id, void* out_rowmajor_host);
 
 /* How lsk_linear_bf16 runs M rows of an [N, K] weight on the current device
- * with a workspace of ws_bytes (0: none): plan[0] = weight rows per output
- * block of the prefill block GEMM (256, 192 or 128), plan[1] = output blocks,
- * plan[2] = blocks whose K range is split over several workgroups, plan[3] =
- * workgroups (K chunks) per split block (1: no split).  plan = {0, 0, 0, 1}
- * whenever the call takes another kernel than the block GEMM, and the plan
- * does not say which: the decode kernels (M <= 16, or N or K off every GEMM
- * tile grid), the 256x256 GEMM with both operands staged in LDS (M > 128,
- * N % 256 == 0, K % 64 == 0 but not a shape the block GEMM takes, e.g. K an
- * odd multiple of 64) or the 128x128 GEMM (the rest of M = 17..128 and of
- * N % 128 == 0, K % 64 == 0).  A workspace smaller than
+ * with a workspace of ws_bytes (0: none).
+ *   17 <= M <= 64, and 65 <= M <= 128 unless N >= 8192 is on the 128-row
+ *   GEMM grid (the skinny kernel; N % 16 == 0, K % 32 == 0): plan[0] =
+ *   weight rows per workgroup (16, 32 or 64), plan[1] = N / plan[0] row
+ *   groups, plan[2] = the groups whose K range is split (all or none),
+ *   plan[3] = workgroups per group (1: no split).  This is the plan of the
+ *   plain and residual epilogues; a SiLU*up call takes whole gate/up pairs
+ *   (32 or 64 rows) and may split differently.
+ *   M > 128: plan[0] = weight rows per output block of the prefill block GEMM
+ *   (256, 192 or 128), plan[1] = output blocks, plan[2] = blocks whose K
+ *   range is split over several workgroups, plan[3] = workgroups (K chunks)
+ *   per split block (1: no split).
+ * plan = {0, 0, 0, 1} whenever the call takes none of those: the decode
+ * kernels (M <= 16, or M > 128 with N or K off every GEMM tile grid), the
+ * 256x256 GEMM with both operands staged in LDS (M > 128, N % 256 == 0,
+ * K % 64 == 0 but not a shape the block GEMM takes, e.g. K an odd multiple of
+ * 64) or the 128x128 GEMM (65 <= M <= 128 with N >= 8192, and the rest of
+ * M > 128 with N % 128 == 0, K % 64 == 0).  A workspace smaller than
  * lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K) is refused with
  * LSK_ERR_WORKSPACE, as lsk_linear_bf16 refuses it.  For tests and tuning; no
  * counterpart in the reference, whose F.linear hides its cuBLAS plan. */
@@ -127,16 +135,20 @@ int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int plan[4]);
  *              SILU_MUL (ldy % 4 == 0, 8-byte aligned)
  *   residual   device bf16 [M][N] at stride ldr, RESIDUAL_ADD only (else NULL)
  *   M          >= 1.  M <= 16 runs the decode/verify kernel (weights streamed
- *              once, activations padded to the 16 MFMA columns); larger M
- *              runs the prefill MFMA GEMM.
- *   workspace  NULL, or (prefill) lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K)
- *              bytes, 256-byte aligned, zero-filled before its first use.
- *              With it, the prefill GEMM splits the K range of the output
- *              blocks of its last, partial round over the idle CUs (split-K)
- *              and adds the fp32 partials in a fixed order; without it, one
- *              workgroup per output block.  Calls
- *              leave it as they found it (see lsk_linear_error); calls that
- *              share one must be stream-ordered.  Ignored for M <= 16.
+ *              once, activations padded to the 16 MFMA columns); 17..128 the
+ *              skinny kernel (weights streamed once, activations in groups
+ *              of 16 tokens; 65..128 rows of N >= 8192 the 128x128 GEMM);
+ *              larger M the prefill MFMA GEMM.
+ *   workspace  NULL, or lsk_workspace_bytes(LSK_OP_LINEAR, M, N, K) bytes
+ *              (0 bytes: no workspace is used), 256-byte aligned, zero-filled
+ *              before its first use.  With it, the prefill GEMM splits the K
+ *              range of the output blocks of its last, partial round over the
+ *              idle CUs (split-K), and the skinny kernel splits the K range
+ *              of every row-block when the row-blocks alone leave CUs idle;
+ *              both add the fp32 partials in a fixed order.  Without it, one
+ *              workgroup per output block.  Calls leave it as they found it
+ *              (see lsk_linear_error); calls that share one must be
+ *              stream-ordered.  Ignored for M <= 16.
  * Replaces torch.mv / F.linear at src/leanstack/runtime/qwen_explicit.py:748,
  * :787, :819, :828-830, :913, :942-948, :1202-1208. */
 int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K,

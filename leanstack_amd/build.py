@@ -23,7 +23,8 @@ INCLUDE = REPO_ROOT / "include"
 BUILD_DIR = PACKAGE_DIR / "_build"
 LIBRARY = PACKAGE_DIR / "libleanstack_amd.so"
 
-SOURCES = ("abi.cpp", "host_rules.cpp", "decode.hip", "gemm.hip", "stack.hip", "attention.hip", "noalloc.hip")
+SOURCES = ("abi.cpp", "host_rules.cpp", "decode.hip", "skinny.hip", "gemm.hip", "stack.hip", "attention.hip",
+           "noalloc.hip")
 OFFLOAD_ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from forming packed FP32 VALU ops.

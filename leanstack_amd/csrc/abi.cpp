@@ -92,6 +92,16 @@ int lsk_abi_version(void) { return LSK_ABI_VERSION; }
 size_t lsk_workspace_bytes(int op, int M, int N, int K) {
   if (op == LSK_OP_LINEAR) {
     if (M <= lsk::kDecodeMaxM || N <= 0 || K <= 0) return 0;
+    if (M <= lsk::kSkinnyMaxM) {
+      // the larger of the plain and the SiLU*up split (lsk_workspace_bytes
+      // does not know the epilogue)
+      if (!lsk::skinny_route(M, N, K)) return 0;
+      int cus = 0;
+      if (lsk::current_device_cus(&cus) != hipSuccess) return 0;
+      const size_t plain = lsk::skinny_plan(M, N, K, false, cus, true).bytes;
+      const size_t silu = N % (2 * lsk::kTileRows) == 0 ? lsk::skinny_plan(M, N, K, true, cus, true).bytes : 0;
+      return plain > silu ? plain : silu;
+    }
     int device = 0;
     if (hipGetDevice(&device) != hipSuccess) return 0;
     hipError_t err;
@@ -113,10 +123,27 @@ int lsk_linear_plan(int M, int N, int K, size_t ws_bytes, int* plan) {
   plan[1] = 0;
   plan[2] = 0;
   plan[3] = 1;
-  // The routing of lsk_linear_bf16: decode kernels up to kDecodeMaxM rows and
-  // off the GEMM tile grid, the block GEMM otherwise.
-  if (M <= lsk::kDecodeMaxM || N % lsk::kGemmBN != 0 || K % lsk::kGemmBK != 0) return LSK_OK;
+  // The routing of lsk_linear_bf16: decode kernels up to kDecodeMaxM rows
+  // (plan {0, 0, 0, 1}); the skinny kernel where skinny_route takes the
+  // shape (plan {weight rows per workgroup, workgroup row groups, groups
+  // split, S}, the plain and residual epilogues' plan); the block GEMM on its
+  // tile grid; decode slices off it ({0, 0, 0, 1}).
+  if (M <= lsk::kDecodeMaxM) return LSK_OK;
   hipError_t err;
+  if (lsk::skinny_route(M, N, K)) {
+    int cus = 0;
+    err = lsk::current_device_cus(&cus);
+    if (err != hipSuccess) return hip_fail(err, "device CU count");
+    lsk::SkinnyPlan p = lsk::skinny_plan(M, N, K, false, cus, ws_bytes > 0);
+    if (p.S > 1 && ws_bytes < p.bytes)
+      return fail(LSK_ERR_WORKSPACE, "projection workspace needs %zu bytes (got %zu)", p.bytes, ws_bytes);
+    plan[0] = p.rows;
+    plan[1] = p.groups;
+    plan[2] = p.S > 1 ? p.groups : 0;
+    plan[3] = p.S;
+    return LSK_OK;
+  }
+  if (N % lsk::kGemmBN != 0 || K % lsk::kGemmBK != 0) return LSK_OK;
   if (ws_bytes > 0) {
     // The workspace lsk_linear_bf16 would refuse is refused here too.
     int device = 0;
@@ -143,6 +170,16 @@ int lsk_linear_bf16(const void* w_packed, int layout_id, int N, int K, const voi
   const bool gemm_shape = N % lsk::kGemmBN == 0 && K % lsk::kGemmBK == 0;
   if (M <= lsk::kDecodeMaxM) {
     err = lsk::launch_decode_linear(w_packed, N, K, x, M, ldx, y, ldy, epi, residual, ldr, stream);
+  } else if (lsk::skinny_route(M, N, K)) {
+    int cus = 0;
+    err = lsk::current_device_cus(&cus);
+    if (err != hipSuccess) return hip_fail(err, "device CU count");
+    const lsk::SkinnyPlan p = lsk::skinny_plan(M, N, K, epi == lsk::Epilogue::kSiluMul, cus, workspace != nullptr);
+    if (p.S > 1 && (ws_bytes < p.bytes || !aligned(workspace, 256)))
+      return fail(LSK_ERR_WORKSPACE, "projection workspace needs %zu bytes, 256-byte aligned (got %zu)", p.bytes,
+                  ws_bytes);
+    err = lsk::launch_skinny_linear(w_packed, N, K, x, M, ldx, y, ldy, epi, residual, ldr,
+                                    p.S > 1 ? workspace : nullptr, ws_bytes, cus, stream);
   } else if (gemm_shape) {
     if (workspace != nullptr) {
       int device = 0;

@@ -28,6 +28,13 @@ constexpr size_t kSkPartialBytes = 256 * 256 * 4;
 constexpr int kSkMaxGrid = (int)((kSkPartialsOffset - kSkFlagsOffset) / 4);
 constexpr unsigned kSkSpinLimit = 1u << 22;
 
+// Projections of kDecodeMaxM < M <= kSkinnyMaxM rows (skinny.hip).
+constexpr int kSkinnyMaxM = 128;
+constexpr int kSkinnyWaves = 8;
+// Split-K arrival counters live in the prefill workspace's flag words (each
+// call leaves them zero), partial slots from kSkPartialsOffset.
+constexpr int kSkinnyMaxGroups = (int)((kSkPartialsOffset - kSkFlagsOffset) / 4);
+
 // Persistent decode-step kernel (stack.hip).
 constexpr int kStackComputeWaves = 8;  // compute waves per workgroup (+1 control wave)
 constexpr int kStackSegTiles = 16;     // k-tiles per K segment of a work pair (K % 512 == 0)
@@ -170,6 +177,24 @@ inline size_t lm_head_workspace_bytes(int M, int V) {
 hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int M, int ldx,
                                  float* logits, int logits_bf16, long long* out_idx,
                                  void* workspace, const void* norm_w, float eps, hipStream_t stream);
+
+// The skinny kernel's plan: `rows` weight rows per workgroup (16, or 32 for a
+// gate/up pair), `groups` = N / rows, each K range split over S workgroups
+// (S > 1 only with a workspace of `bytes` bytes), for a device of `cus` CUs.
+struct SkinnyPlan {
+  int rows, groups, S;
+  size_t bytes;
+};
+int skinny_groups(int M);
+hipError_t current_device_cus(int* cus_out);
+bool skinny_route(int M, int N, int K);
+SkinnyPlan skinny_plan(int M, int N, int K, bool silu, int cus, bool has_workspace);
+// y = epilogue(x . W^T) for kDecodeMaxM < M <= kSkinnyMaxM (N % 16 == 0, or
+// N % 32 == 0 for SiLU*up; K % 32 == 0).  `workspace` (NULL: no split) must
+// hold skinny_plan(...).bytes bytes, flags zero (every call leaves them zero).
+hipError_t launch_skinny_linear(const void* w, int N, int K, const void* x, int M, int ldx, void* y, int ldy,
+                                Epilogue epi, const void* residual, int ldr, void* workspace, size_t ws_bytes,
+                                int cus, hipStream_t stream);
 
 // Records a HIP failure for lsk_last_error (defined in abi.cpp).
 int fail_hip_call(hipError_t err, const char* what);

@@ -595,8 +595,9 @@ def test_prefill_m8192_sampled_rows(gpu, name):
 
 def _random_shapes(count: int, seed: int) -> list[tuple[int, int, int, int]]:
     """(M, N, K, epilogue) drawn over every routing class of lsk_linear_bf16:
-    decode (M <= 16), decode slices (N or K off the block GEMM's grid),
-    the 128-row GEMM, and the block GEMM with and without a split last round."""
+    decode (M <= 16), the skinny kernel (M = 17..128), decode slices (N or K
+    off the block GEMM's grid, M > 128), the 128-row GEMM, and the block GEMM
+    with and without a split last round."""
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
