@@ -27,7 +27,6 @@
 
 #include <hip/hip_runtime.h>
 
-#include <cstdlib>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -378,10 +377,6 @@ SkinnyPlan skinny_plan(int M, int N, int K, bool silu, int cus, bool has_workspa
     if (S > max_s) S = max_s;
     if (S < 1) S = 1;
   }
-#ifdef LSK_SKINNY_FORCE
-  if (const char* e = getenv("LSK_SKINNY_RBW")) rbw = atoi(e);
-  if (const char* e = getenv("LSK_SKINNY_S")) S = has_workspace ? atoi(e) : 1;
-#endif
   SkinnyPlan p;
   p.rows = kTileRows * rbw;
   p.groups = NB / rbw;
