@@ -244,6 +244,93 @@ def step_kernel_durations(kernels, stack, g, reps: int) -> dict[str, list[float]
     return {name: durs[i::4] for i, name in enumerate(g.projections())}
 
 
+def probe_step_floor(torch, steps: int, warmup: int) -> dict:
+    """What a decode step's launch structure can reach, measured with
+    lsk_probe_stream_step on the step's exact weight bytes (36 layers x
+    {qkv, o, gate_up, down}, each CU streaming an equal share of each
+    projection, every tile multiplied, nothing else computed): one
+    persistent launch with no dependency between projections, with a flat
+    grid barrier before each, with the two-level barrier; and a HIP graph of
+    144 single-projection launches of the same kernel (the structure of the
+    product step).  Each launch timed with events on its stream, median of
+    `steps` after `warmup`."""
+    import ctypes
+
+    from leanstack_amd import _lib
+    from leanstack_amd.geometry import QWEN3_4B as G
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    per_layer = [n * k // 512 for n, k in G.projections().values()]  # 1 KB tiles (512 bf16 values)
+    seg = per_layer * G.num_hidden_layers
+    if any(t % cus for t in seg):
+        raise SystemExit(f"projection tile counts {per_layer} are not multiples of the {cus} CUs")
+    total = sum(seg) * 1024
+    weights = torch.empty(total, dtype=torch.uint8, device=dev)
+    weights.view(torch.int16).random_(-2000, 2000)  # small finite bf16 values
+    ws = torch.zeros(lib.lsk_probe_workspace_bytes(), dtype=torch.uint8, device=dev)
+    arr = (ctypes.c_longlong * len(seg))(*seg)
+
+    def launch(mode, ring, segs=arr, count=len(seg), base=weights.data_ptr(), nbytes=total):
+        st = lib.lsk_probe_stream_step(base, nbytes, segs, count, mode, ring, ws.data_ptr(), ws.numel(),
+                                       torch.cuda.current_stream().cuda_stream)
+        _lib.check(st, "lsk_probe_stream_step")
+
+    def timed(fn) -> float:
+        for _ in range(warmup):
+            fn()
+        out = []
+        for _ in range(steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            out.append(a.elapsed_time(b) * 1e3)
+        return statistics.median(out)
+
+    res = {"bytes": total, "projections": len(seg), "cus": cus}
+    for name, mode, ring in (("one_launch_no_dependency_ring4", 0, 4), ("one_launch_no_dependency_ring16", 0, 16),
+                             ("one_launch_flat_barrier_ring4", 1, 4), ("one_launch_two_level_barrier_ring4", 2, 4),
+                             ("one_launch_two_level_barrier_ring16", 2, 16)):
+        us = timed(lambda: launch(mode, ring))
+        torch.cuda.synchronize()
+        if int(ws[:4].view(torch.int32).item()) != 0:
+            raise SystemExit(f"probe {name}: a bounded wait gave up")
+        res[name] = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1)}
+        log(f"probe {name}: {us:.1f} us, {total / (us * 1e-6) / 1e9:.0f} GB/s")
+    # 144 dependent launches, one projection each, captured as one graph
+    offsets, off = [], 0
+    singles = []
+    for t in seg:
+        singles.append((ctypes.c_longlong * 1)(t))
+        offsets.append(off)
+        off += t * 1024
+
+    def graph_step():
+        for t, o, one in zip(seg, offsets, singles):
+            launch(0, 4, segs=one, count=1, base=weights.data_ptr() + o, nbytes=t * 1024)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        graph_step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        graph_step()
+    us = timed(graph.replay)
+    res["graph_of_144_launches_ring4"] = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1)}
+    log(f"probe graph of 144 launches: {us:.1f} us, {total / (us * 1e-6) / 1e9:.0f} GB/s")
+    base = res["one_launch_no_dependency_ring4"]["us"]
+    for name in ("one_launch_flat_barrier_ring4", "one_launch_two_level_barrier_ring4",
+                 "one_launch_two_level_barrier_ring16", "graph_of_144_launches_ring4"):
+        res[name]["us_per_boundary_over_no_dependency"] = round((res[name]["us"] - base) / (len(seg) - 1), 2)
+    return res
+
+
 def mean(values: list[float]) -> float:
     return sum(values) / len(values)
 
@@ -264,6 +351,10 @@ def main() -> int:
                          "36-launch graph replays, the four prefill GEMMs at M = 2048 over 8-launch replays), for "
                          "profiling with rocprofv3 --kernel-trace --stats: the trace then holds exactly their "
                          "dispatches")
+    ap.add_argument("--probe-step-floor", action="store_true",
+                    help="only the launch-structure probe (lsk_probe_stream_step): the step's weight bytes streamed "
+                         "by one persistent launch with and without a grid barrier per projection, and by a graph "
+                         "of 144 single-projection launches")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
                          "M = 2048 and 8192, three launches each, no graphs")
@@ -288,6 +379,10 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     steps, warmup = args.steps, args.warmup
+
+    if args.probe_step_floor:
+        print(json.dumps({"probe_step_floor": probe_step_floor(torch, max(steps, 5), max(warmup, 2))}), flush=True)
+        return 0
 
     # --- resident weights: 36 layers + lm_head in one arena ------------------
     t0 = time.perf_counter()

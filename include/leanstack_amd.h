@@ -370,6 +370,26 @@ void lsk_set_linear_wait_limit(unsigned polls);
 int lsk_dispatch_timing_begin(int max_dispatches);
 int lsk_dispatch_timing_end(float* durations_us, int capacity, int* dispatches);
 
+/* Measurement of what a single-launch decode step could reach (bench.py
+ * --probe-step-floor).  One persistent workgroup per CU streams `count`
+ * segments of 1 KB tiles from `weights` (sum(seg_tiles) * 1024 bytes, any
+ * contents; each seg_tiles[s], host, a multiple of the CU count and at
+ * least 12 per CU)
+ * through 12 compute waves holding `ring` (4 or 16) tile loads each in
+ * flight, every CU taking an equal contiguous share of each segment and
+ * multiplying every tile.  mode 0: no dependency between segments; mode 1:
+ * before the first multiply of segment s + 1 every workgroup waits until all
+ * have finished segment s, on one arrival word per segment; mode 2: the same
+ * on a two-level barrier (8 group words, the last arrival of each group
+ * counts globally and releases its group).  The weight loads run ahead
+ * across the waits.  workspace: lsk_probe_workspace_bytes() bytes,
+ * zero-filled before first use; every launch leaves it zero except word 0,
+ * which is nonzero after a bounded wait gave up.  No counterpart in the
+ * reference. */
+size_t lsk_probe_workspace_bytes(void);
+int lsk_probe_stream_step(const void* weights, size_t weight_bytes, const long long* seg_tiles, int count, int mode,
+                          int ring, void* workspace, size_t ws_bytes, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,7 @@ BUILD_DIR = PACKAGE_DIR / "_build"
 LIBRARY = PACKAGE_DIR / "libleanstack_amd.so"
 
 SOURCES = ("abi.cpp", "host_rules.cpp", "decode.hip", "skinny.hip", "gemm.hip", "stack.hip", "attention.hip",
-           "noalloc.hip")
+           "noalloc.hip", "probe.hip")
 OFFLOAD_ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from forming packed FP32 VALU ops.

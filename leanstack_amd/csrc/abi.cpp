@@ -469,6 +469,40 @@ int lsk_stack_error(void* workspace, int* error_out) {
   return read_clear_error_word(workspace, lsk::kStackWsError, error_out);
 }
 
+size_t lsk_probe_workspace_bytes(void) { return lsk::kProbeWsBytes; }
+
+int lsk_probe_stream_step(const void* weights, size_t weight_bytes, const long long* seg_tiles, int count, int mode,
+                          int ring, void* workspace, size_t ws_bytes, void* hip_stream) {
+  lsk::clear_error();
+  if (weights == nullptr || !aligned(weights, 16)) return fail(LSK_ERR_INVALID, "weights must be 16-byte aligned");
+  if (seg_tiles == nullptr || count < 1 || count > lsk::kProbeMaxSegments)
+    return fail(LSK_ERR_INVALID, "count=%d segments must be in 1..%d", count, lsk::kProbeMaxSegments);
+  if (mode < 0 || mode > 2) return fail(LSK_ERR_INVALID, "mode=%d must be 0, 1 or 2", mode);
+  if (ring != 4 && ring != 16) return fail(LSK_ERR_INVALID, "ring=%d must be 4 or 16", ring);
+  if (workspace == nullptr || ws_bytes < lsk::kProbeWsBytes || !aligned(workspace, 4))
+    return fail(LSK_ERR_WORKSPACE, "probe workspace needs %zu bytes (got %zu)", lsk::kProbeWsBytes, ws_bytes);
+  int cus = 0;
+  hipError_t err = lsk::current_device_cus(&cus);
+  if (err != hipSuccess) return hip_fail(err, "device CU count");
+  lsk::ProbeSegments seg{};
+  seg.count = count;
+  unsigned long long total = 0;
+  for (int i = 0; i < count; ++i) {
+    const long long t = seg_tiles[i];
+    if (t <= 0 || t % cus != 0 || t / cus < lsk::kProbeComputeWaves || t / cus > (1 << 30))
+      return fail(LSK_ERR_INVALID, "segment %d: %lld tiles must be a multiple of the %d CUs, at least %d per CU", i,
+                  t, cus, lsk::kProbeComputeWaves);
+    seg.per_cu[i] = (int)(t / cus);
+    seg.first[i] = total;
+    total += (unsigned long long)t;
+  }
+  if (total * 1024ull > weight_bytes)
+    return fail(LSK_ERR_INVALID, "%llu tiles need %llu weight bytes (got %zu)", total, total * 1024ull, weight_bytes);
+  err = lsk::launch_probe_step(weights, seg, mode, ring, cus, workspace, static_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess) return hip_fail(err, "probe kernel launch");
+  return LSK_OK;
+}
+
 int lsk_dispatch_timing_begin(int max_dispatches) {
   lsk::DispatchTiming& t = lsk::dispatch_timing();
   if (t.active) return fail(LSK_ERR_INVALID, "a dispatch timing is already active on this thread");

@@ -196,6 +196,29 @@ hipError_t launch_skinny_linear(const void* w, int N, int K, const void* x, int 
                                 Epilogue epi, const void* residual, int ldr, void* workspace, size_t ws_bytes,
                                 int cus, hipStream_t stream);
 
+// The step-streaming probe (probe.hip, lsk_probe_stream_step): segment s has
+// per_cu[s] 1 KB tiles per workgroup starting at tile first[s] + g * per_cu[s].
+constexpr int kProbeComputeWaves = 12;
+constexpr int kProbeMaxSegments = 256;
+struct ProbeSegments {
+  int count;
+  int per_cu[kProbeMaxSegments];
+  unsigned long long first[kProbeMaxSegments];
+};
+// Workspace words: error, exit counter, checksum sink, the global arrival
+// word, 8 group words (16 apart), one flat arrival word per segment, 8 go
+// words per segment.
+constexpr int kProbeWsError = 0;
+constexpr int kProbeWsExit = 1;
+constexpr int kProbeWsSink = 2;
+constexpr int kProbeWsGlobal = 16;
+constexpr int kProbeWsGroups = 64;
+constexpr int kProbeWsFlat = 256;
+constexpr int kProbeWsGo = kProbeWsFlat + kProbeMaxSegments;
+constexpr size_t kProbeWsBytes = (size_t)(kProbeWsGo + 8 * kProbeMaxSegments) * 4;
+hipError_t launch_probe_step(const void* weights, const ProbeSegments& seg, int mode, int ring, int grid,
+                             void* workspace, hipStream_t stream);
+
 // Records a HIP failure for lsk_last_error (defined in abi.cpp).
 int fail_hip_call(hipError_t err, const char* what);
 

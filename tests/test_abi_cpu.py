@@ -313,3 +313,23 @@ def test_linear_plan_rejects_and_routes_without_a_device():
         plan = (ctypes.c_int * 4)(9, 9, 9, 9)
         assert lib.lsk_linear_plan(m, n, k, 1 << 26, plan) == _lib.OK
         assert list(plan) == [0, 0, 0, 1], (m, n, k, list(plan))
+
+
+def test_probe_rejects_before_launch():
+    """The launch-structure probe refuses bad arguments before touching the
+    GPU: no segments, an unknown mode or ring depth, a small workspace."""
+    lib = _lib.load()
+    need = lib.lsk_probe_workspace_bytes()
+    assert need >= 4 * (256 + 256 + 8 * 256)
+    segs = (ctypes.c_longlong * 2)(256 * 12, 256 * 12)
+    fake = 1 << 20  # never dereferenced: every case fails validation first
+
+    def call(count=2, mode=0, ring=4, ws_bytes=need, weights=fake):
+        return lib.lsk_probe_stream_step(weights, 1 << 30, segs, count, mode, ring, fake, ws_bytes, None)
+
+    assert call(count=0) == _lib.ERR_INVALID
+    assert call(count=257) == _lib.ERR_INVALID
+    assert call(mode=3) == _lib.ERR_INVALID
+    assert call(ring=8) == _lib.ERR_INVALID
+    assert call(weights=fake + 8) == _lib.ERR_INVALID
+    assert call(ws_bytes=need - 4) == _lib.ERR_WORKSPACE
