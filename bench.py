@@ -331,6 +331,43 @@ def probe_step_floor(torch, steps: int, warmup: int) -> dict:
     return res
 
 
+def probe_mfma(torch, steps: int, warmup: int) -> dict:
+    """The dense BF16 MFMA rate with no memory traffic (lsk_probe_mfma_rate):
+    4 waves per workgroup, 16 accumulator tiles of v_mfma_f32_32x32x16_bf16
+    each (the prefill GEMM's instruction and accumulators), on every CU (one
+    workgroup per CU; launches of about 3.5 and 35 ms) and on 32 CUs;
+    TFLOP/s = 32768 FLOP x 64 MFMAs x iterations x waves / time (HIP events,
+    median of `steps`)."""
+    from leanstack_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    res = {"cus": cus, "mfma": "v_mfma_f32_32x32x16_bf16", "flop_per_mfma": 32768}
+    for wgs, iterations in ((cus, 4000), (32, 4000), (cus, 40000)):
+        def run():
+            _lib.check(lib.lsk_probe_mfma_rate(wgs, iterations, sink.data_ptr(), torch.cuda.current_stream().cuda_stream),
+                       "lsk_probe_mfma_rate")
+        for _ in range(warmup):
+            run()
+        times = []
+        for _ in range(steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            run()
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) * 1e3)
+        us = statistics.median(times)
+        flops = 32768.0 * 64 * iterations * 4 * wgs
+        key = f"workgroups_{wgs}_iterations_{iterations}"
+        res[key] = {"us": round(us, 1), "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1),
+                    "frac_of_2.5PF_scaled_to_CUs": round(flops / (us * 1e-6) / 1e12 / (BF16_PEAK_TFLOPS * wgs / cus), 4)}
+        log(f"probe mfma on {wgs} workgroups x {iterations} iterations: {us:.1f} us, {res[key]['TFLOP/s']} TFLOP/s")
+    return res
+
+
 def mean(values: list[float]) -> float:
     return sum(values) / len(values)
 
@@ -355,6 +392,9 @@ def main() -> int:
                     help="only the launch-structure probe (lsk_probe_stream_step): the step's weight bytes streamed "
                          "by one persistent launch with and without a grid barrier per projection, and by a graph "
                          "of 144 single-projection launches")
+    ap.add_argument("--probe-mfma", action="store_true",
+                    help="only the MFMA-rate probe (lsk_probe_mfma_rate): dense BF16 MFMAs with no memory traffic, "
+                         "on every CU and on 32")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
                          "M = 2048 and 8192, three launches each, no graphs")
@@ -380,6 +420,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     steps, warmup = args.steps, args.warmup
 
+    if args.probe_mfma:
+        print(json.dumps({"probe_mfma": probe_mfma(torch, max(steps, 5), max(warmup, 2))}), flush=True)
+        return 0
     if args.probe_step_floor:
         print(json.dumps({"probe_step_floor": probe_step_floor(torch, max(steps, 5), max(warmup, 2))}), flush=True)
         return 0

@@ -387,6 +387,13 @@ int lsk_dispatch_timing_end(float* durations_us, int capacity, int* dispatches);
  * which is nonzero after a bounded wait gave up.  No counterpart in the
  * reference. */
 size_t lsk_probe_workspace_bytes(void);
+/* Measurement of the dense BF16 MFMA rate (bench.py --probe-mfma): each of
+ * `workgroups` workgroups of 4 waves runs `iterations` x 64
+ * v_mfma_f32_32x32x16_bf16 (16 accumulator tiles per wave, operands in
+ * registers, 32768 FLOP each), with no memory traffic.  sink: one device
+ * word, written only if a checksum takes a value it never takes.  No
+ * counterpart in the reference. */
+int lsk_probe_mfma_rate(int workgroups, int iterations, void* sink, void* hip_stream);
 int lsk_probe_stream_step(const void* weights, size_t weight_bytes, const long long* seg_tiles, int count, int mode,
                           int ring, void* workspace, size_t ws_bytes, void* hip_stream);
 

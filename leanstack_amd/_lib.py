@@ -121,6 +121,7 @@ _SIGNATURES.update({
     "lsk_dispatch_timing_begin": (_c_int, [_c_int]),
     "lsk_dispatch_timing_end": (_c_int, [ctypes.POINTER(ctypes.c_float), _c_int, ctypes.POINTER(_c_int)]),
     "lsk_probe_workspace_bytes": (_c_size, []),
+    "lsk_probe_mfma_rate": (_c_int, [_c_int, _c_int, _c_void, _c_void]),
     "lsk_probe_stream_step": (
         _c_int, [_c_void, _c_size, ctypes.POINTER(ctypes.c_longlong), _c_int, _c_int, _c_int, _c_void, _c_size, _c_void]),
 })

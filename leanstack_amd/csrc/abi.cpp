@@ -503,6 +503,16 @@ int lsk_probe_stream_step(const void* weights, size_t weight_bytes, const long l
   return LSK_OK;
 }
 
+int lsk_probe_mfma_rate(int workgroups, int iterations, void* sink, void* hip_stream) {
+  lsk::clear_error();
+  if (workgroups < 1 || workgroups > 65536 || iterations < 1 || iterations > (1 << 24))
+    return fail(LSK_ERR_INVALID, "workgroups=%d (1..65536) and iterations=%d (1..2^24)", workgroups, iterations);
+  if (sink == nullptr || !aligned(sink, 4)) return fail(LSK_ERR_INVALID, "sink must be a 4-byte aligned device word");
+  const hipError_t err = lsk::launch_probe_mfma(workgroups, iterations, sink, static_cast<hipStream_t>(hip_stream));
+  if (err != hipSuccess) return hip_fail(err, "probe kernel launch");
+  return LSK_OK;
+}
+
 int lsk_dispatch_timing_begin(int max_dispatches) {
   lsk::DispatchTiming& t = lsk::dispatch_timing();
   if (t.active) return fail(LSK_ERR_INVALID, "a dispatch timing is already active on this thread");

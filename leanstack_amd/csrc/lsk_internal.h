@@ -218,6 +218,7 @@ constexpr int kProbeWsGo = kProbeWsFlat + kProbeMaxSegments;
 constexpr size_t kProbeWsBytes = (size_t)(kProbeWsGo + 8 * kProbeMaxSegments) * 4;
 hipError_t launch_probe_step(const void* weights, const ProbeSegments& seg, int mode, int ring, int grid,
                              void* workspace, hipStream_t stream);
+hipError_t launch_probe_mfma(int workgroups, int iterations, void* sink, hipStream_t stream);
 
 // Records a HIP failure for lsk_last_error (defined in abi.cpp).
 int fail_hip_call(hipError_t err, const char* what);

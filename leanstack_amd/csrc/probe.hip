@@ -1,6 +1,7 @@
-// Measurement kernel for the decode step's launch structure:
-// lsk_probe_stream_step.  No counterpart in the reference; bench.py
-// --probe-step-floor runs it.
+// Measurement kernels: lsk_probe_stream_step (the decode step's launch
+// structure, bench.py --probe-step-floor) and lsk_probe_mfma_rate (the dense
+// BF16 MFMA rate with no memory traffic, bench.py --probe-mfma).  No
+// counterpart in the reference.
 //
 // It answers one question about a single-launch (persistent) decode step:
 // how fast can one workgroup per CU stream a step's weight bytes when every
@@ -187,7 +188,64 @@ __global__ __launch_bounds__((kW + 1) * 64, 1) void probe_step_kernel(const char
   }
 }
 
+// The MFMA rate with nothing else to do: 4 waves per workgroup, each with
+// 16 accumulator tiles of v_mfma_f32_32x32x16_bf16 (the prefill GEMM's
+// instruction and accumulator count), 64 back-to-back MFMAs per iteration.
+// The operands cycle through 8 A and 8 B fragments of pseudo-random bf16
+// values in [1, 2) with random signs and mantissas, so the multipliers switch
+// as they do on data (power, and with it the clock, depends on that).  A
+// checksum store nobody expects keeps the work.
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ unsigned probe_hash(unsigned v) {
+  v ^= v >> 16;
+  v *= 0x7feb352du;
+  v ^= v >> 15;
+  v *= 0x846ca68bu;
+  v ^= v >> 16;
+  return v;
+}
+__device__ __forceinline__ bf16x8_t probe_fragment(unsigned seed) {
+  u32x4_t v;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned h = probe_hash(seed * 4u + (unsigned)i);
+    // two bf16 values: sign and 7 mantissa bits random, exponent of [1, 2)
+    v[i] = (0x3f80u | (h & 0x807fu)) | ((0x3f80u | ((h >> 16) & 0x807fu)) << 16);
+  }
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+__global__ __launch_bounds__(256, 1) void probe_mfma_kernel(int iterations, unsigned* __restrict__ sink) {
+  const unsigned id = blockIdx.x * 256u + threadIdx.x;
+  bf16x8_t a[8], b[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = probe_fragment(id * 16u + (unsigned)i);
+    b[i] = probe_fragment(id * 16u + 8u + (unsigned)i);
+  }
+  f32x16_t acc[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[t][e] = 0.f;
+  for (int it = 0; it < iterations; ++it) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[(t + r) & 7], b[(3 * t + r) & 7], acc[t], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < 16; ++t) s += acc[t][threadIdx.x & 15];
+  if (s == 1.5e-38f) st_agent(sink, 1u);
+}
+
 }  // namespace
+
+hipError_t launch_probe_mfma(int workgroups, int iterations, void* sink, hipStream_t stream) {
+  launch_kernel(probe_mfma_kernel, dim3(workgroups), dim3(256), 0, stream, iterations, static_cast<unsigned*>(sink));
+  return hipGetLastError();
+}
 
 hipError_t launch_probe_step(const void* weights, const ProbeSegments& seg, int mode, int ring, int grid,
                              void* workspace, hipStream_t stream) {

@@ -35,3 +35,15 @@ def test_probe_modes_complete(gpu, mode, ring):
     short = (ctypes.c_longlong * 1)(cus * 11)
     assert lib.lsk_probe_stream_step(weights.data_ptr(), weights.numel(), short, 1, mode, ring, ws.data_ptr(),
                                      ws.numel(), None) == _lib.ERR_INVALID
+
+
+def test_probe_mfma_runs(gpu):
+    """The MFMA-rate probe completes, leaves its sink alone, and refuses bad
+    arguments before launch."""
+    lib = _lib.load()
+    sink = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda:0"))
+    assert lib.lsk_probe_mfma_rate(8, 10, sink.data_ptr(), torch.cuda.current_stream().cuda_stream) == _lib.OK
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    assert lib.lsk_probe_mfma_rate(0, 10, sink.data_ptr(), None) == _lib.ERR_INVALID
+    assert lib.lsk_probe_mfma_rate(8, 0, sink.data_ptr(), None) == _lib.ERR_INVALID
