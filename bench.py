@@ -397,7 +397,7 @@ def main() -> int:
                          "on every CU and on 32")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
-                         "M = 2048 and 8192, three launches each, no graphs")
+                         "M = 512, 2048 and 8192, three launches each, no graphs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
@@ -497,7 +497,7 @@ def main() -> int:
     if args.pmc_prefill:
         p0 = layers[0]
         weights = {"qkv_proj": p0.qkv, "o_proj": p0.o, "gate_up_proj": p0.gate_up, "down_proj": p0.down}
-        for m in (2048, 8192):
+        for m in (512, 2048, 8192):
             for name, pw in weights.items():
                 x = torch.randn((m, pw.k), generator=gen, device=dev).to(torch.bfloat16)
                 epi = _lib.EPI_SILU_MUL if name == "gate_up_proj" else _lib.EPI_NONE
