@@ -309,6 +309,9 @@ __host__ __device__ constexpr int staged_wave_bytes(int U, int M, int RBW) {
 // NORM value of the kernels' staged-activation form with NC chunks per lane
 // (NORM = 0: fragments loaded per tile; > 0 and -1: the RMSNorm prologues).
 constexpr int staged_x(int nc) { return -1 - nc; }
+// The same with the wave's x slice staged in two phases (NC chunks per lane
+// per phase): decode_linear_kernel only.
+constexpr int staged_x2(int nc) { return -101 - nc; }
 
 // Single-round accumulate_rows with the wave's slice of x -- M rows x U*32
 // values, M*U*4 chunks of 8 -- loaded densely (NC chunks per lane, one
@@ -318,24 +321,42 @@ constexpr int staged_x(int nc) { return -1 - nc; }
 // as many vector-memory requests as the weight tiles themselves.  HALF: the
 // half-block fragment order (see accumulate_rows_rms_dense).  No barrier:
 // each wave reads only its own area.
-template <int NW, int RBW, int U, int NC, bool HALF>
+template <int NW, int RBW, int U, int NC, bool HALF, int PH = 1>
 __device__ __forceinline__ void accumulate_rows_staged(f32x4_t (&acc)[RBW], const bf16x8_t* __restrict__ wt,
                                                        const __bf16* __restrict__ x, int ldx, int M, int KT, int kb,
                                                        int wave, int lane) {
-  constexpr int kRowChunks = U * 4;
+  static_assert(PH == 1 || (PH == 2 && !HALF), "two-phase staging is for the 16-row form");
   constexpr int kRowStride = U * 32 + 8;
   __bf16* xs = reinterpret_cast<__bf16*>(rms_lds + (size_t)wave * staged_wave_bytes(U, M, RBW));
-  const int C = M * kRowChunks;
   const int m = lane & 15;
   const int g = lane >> 4;
+  // Phase p stages k-tiles [kt0(p), kt0(p + 1)) of the wave's slice: M rows
+  // of (kt1 - kt0) * 4 chunks of 8 values, NC chunks per lane.
+  auto kt0 = [](int p) { return p * U / PH; };
   bf16x8_t xd[NC];
+  auto load_phase = [&](int p) {
+    const int pc = (kt0(p + 1) - kt0(p)) * 4;
+    const int C = M * pc;
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = min(lane + 64 * i, C - 1);  // lanes past the last chunk reload it
-    const int mc = c / kRowChunks;
-    const int j = c - mc * kRowChunks;
-    xd[i] = *reinterpret_cast<const bf16x8_t*>(x + (size_t)mc * ldx + (kb * 4 + j) * 8);
-  }
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(lane + 64 * i, C - 1);  // lanes past the last chunk reload it
+      const int mc = c / pc;
+      const int j = kt0(p) * 4 + c - mc * pc;
+      xd[i] = *reinterpret_cast<const bf16x8_t*>(x + (size_t)mc * ldx + (kb * 4 + j) * 8);
+    }
+  };
+  auto store_phase = [&](int p) {
+    const int pc = (kt0(p + 1) - kt0(p)) * 4;
+    const int C = M * pc;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int c = min(lane + 64 * i, C - 1);
+      const int mc = c / pc;
+      const int j = kt0(p) * 4 + c - mc * pc;
+      *reinterpret_cast<bf16x8_t*>(xs + mc * kRowStride + j * 8) = xd[i];
+    }
+  };
+  load_phase(0);
   __builtin_amdgcn_sched_barrier(0);
   constexpr int kLoads = HALF ? U / 2 : U;
   bf16x8_t wv[kLoads][RBW];
@@ -346,13 +367,7 @@ __device__ __forceinline__ void accumulate_rows_staged(f32x4_t (&acc)[RBW], cons
       wv[u][r] = load_weight_tile(wt + ((size_t)r * KT + kb + (HALF ? 2 * u : u)) * 64);
   }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int c = min(lane + 64 * i, C - 1);
-    const int mc = c / kRowChunks;
-    const int j = c - mc * kRowChunks;
-    *reinterpret_cast<bf16x8_t*>(xs + mc * kRowStride + j * 8) = xd[i];
-  }
+  store_phase(0);
   if constexpr (HALF) {
     const int hi = m >= M && m < 2 * M ? 1 : 0;
     const int row = m < M ? m : (hi ? m - M : M - 1);
@@ -364,11 +379,18 @@ __device__ __forceinline__ void accumulate_rows_staged(f32x4_t (&acc)[RBW], cons
     }
   } else {
     const int mr = m < M ? m : M - 1;  // padding columns: finite, never stored
+    // The second phase's chunks load while the first phase multiplies (they
+    // queue behind the weight loads, which the first multiplies wait for).
+    if constexpr (PH == 2) load_phase(1);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + mr * kRowStride + u * 32 + g * 8);
+    for (int p = 0; p < PH; ++p) {
+      if (p == 1) store_phase(1);
 #pragma unroll
-      for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+      for (int u = kt0(p); u < kt0(p + 1); ++u) {
+        const bf16x8_t xn = *reinterpret_cast<const bf16x8_t*>(xs + mr * kRowStride + u * 32 + g * 8);
+#pragma unroll
+        for (int r = 0; r < RBW; ++r) acc[r] = mfma16(wv[u][r], xn, acc[r]);
+      }
     }
   }
 }
@@ -511,6 +533,10 @@ __global__ __launch_bounds__(NW * 64) void decode_linear_kernel(
   } else if constexpr (NORM == -1) {
     const bf16x8_t* nrow = reinterpret_cast<const bf16x8_t*>(norm_w) + g;
     accumulate_rows_rms<NW, RBW>(acc, wt, xrow, nrow, m_active, KT, kb, ke, wave, lane, eps);
+  } else if constexpr (NORM < -100) {
+    (void)norm_w;
+    (void)eps;
+    accumulate_rows_staged<NW, RBW, U, -101 - NORM, false, 2>(acc, wt, x, ldx, M, KT, kb, wave, lane);
   } else if constexpr (NORM < -1) {
     (void)norm_w;
     (void)eps;
@@ -972,7 +998,13 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
   }
   if constexpr (RBW == 1) {
     if (a.KT == 128 && a.M <= 8) return launch_staged<8, RBW, EPI, 16, false>(a, a.M, stream);
-    if (a.KT == 304 && a.M <= 6) return launch_staged<16, RBW, EPI, 19, false>(a, (76 * a.M + 63) / 64, stream);
+    if (a.KT == 304 && a.M <= 5) return launch_staged<16, RBW, EPI, 19, false>(a, (76 * a.M + 63) / 64, stream);
+    // M = 6..8: in two phases (10 + 9 k-tiles, 4 or 5 chunks per lane each),
+    // so the chunk registers fit beside the 19 weight tiles (8-10 chunks in
+    // one phase spill): 13.7-14.3 -> 11.5-11.9 us per launch; at M = 5 the
+    // single phase (6 chunks) is 0.3 us faster.
+    if (a.KT == 304 && a.M <= 6) return launch_decode_cfg<16, RBW, EPI, 19, staged_x2(4)>(a, stream);
+    if (a.KT == 304 && a.M <= 8) return launch_decode_cfg<16, RBW, EPI, 19, staged_x2(5)>(a, stream);
   }
   if (a.KT == 80 && a.M <= 8) {
     if constexpr (RBW == 1) return launch_half_cfg<8, RBW, EPI, 5>(a, stream);
