@@ -12,7 +12,8 @@ activations read + outputs written) / step time, in GB/s.
 Also reported (under "detail"): the verify sweep M = 1, 2, 4, 8 over the same
 stack, the step with the two RMSNorms of each layer (fused into the QKV and
 gate_up kernels, or as separate F.rms_norm launches), a whole decode token with
-attention over 320 and 4095 cached rows (every layer HIP), each projection kind's
+attention over 320 and 4095 cached rows (every layer HIP), a greedy decode loop of
+256 tokens (one graph replay per token, per-step events), each projection kind's
 per-launch time, the tied lm_head + argmax at M = 1..8, and the prefill GEMMs
 at M = 512, 2048, 8192 in TFLOP/s.
 
@@ -580,7 +581,52 @@ def main() -> int:
         ms = time_graph(torch, graph, steps, warmup)
         token_steps[pos] = {"us": round(ms * 1e3, 1), "tokens_per_s": round(1e3 / ms, 1)}
         log(f"decode token with attention over {pos} cached rows: {ms * 1e3:.1f} us ({1e3 / ms:.0f} tokens/s)")
-    del graph, token_step, k_cache, v_cache
+    del graph
+
+    # --- a greedy decode loop: each token the argmax of the one before -------
+    # The reference's decode loop (qwen_explicit_runtime_loop.py:331-385) with
+    # its per-step events: here one graph of DecodeStep.launch_next (embedding
+    # row of the last token, the 36 layers, the head, token record, position
+    # advance) is replayed once per token, with a pair of events around each
+    # replay and one pair around the loop. The loop runs twice from the same
+    # start (same first token, position and cache rows below it): the second
+    # run must emit the same tokens.
+    loop_tokens, loop_start = 256, 320
+    embedding = (0.02 * torch.randn((G.vocab_size, G.hidden_size), generator=gen, device=dev)).to(torch.bfloat16)
+    emitted = torch.full((kv_rows,), -1, device=dev, dtype=torch.long)
+    graph = stack.capture(lambda: token_step.launch_next(embedding, emitted))
+    runs = []
+    for _ in range(2):
+        token_step.token.fill_(1)
+        token_step.set_position(loop_start)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(loop_tokens)]
+        loop_ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        loop_ev[0].record()
+        for a, b in ev:
+            a.record()
+            graph.replay()
+            b.record()
+        loop_ev[1].record()
+        torch.cuda.synchronize()
+        step_us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+        runs.append((loop_ev[0].elapsed_time(loop_ev[1]) * 1e3, step_us,
+                     emitted[loop_start:loop_start + loop_tokens].cpu()))
+    del graph, embedding, token_step, k_cache, v_cache
+    loop_us, step_us, toks = runs[1]
+    if not torch.equal(runs[0][2], toks) or int(toks.min()) < 0:
+        raise SystemExit("greedy decode loop: the two runs from the same start emitted different tokens")
+    greedy_loop = {
+        "tokens": loop_tokens, "first_position": loop_start, "loop_us": round(loop_us, 1),
+        "tokens_per_s": round(loop_tokens / (loop_us * 1e-6), 1),
+        "step_us_median": round(step_us[len(step_us) // 2], 1), "step_us_p10": round(step_us[len(step_us) // 10], 1),
+        "step_us_p90": round(step_us[len(step_us) * 9 // 10], 1), "distinct_tokens": int(toks.unique().numel()),
+        "repeatable": True,
+    }
+    log(f"greedy decode loop, {loop_tokens} tokens from position {loop_start}: {loop_us / loop_tokens:.1f} us/token "
+        f"({greedy_loop['tokens_per_s']} tokens/s), step median {greedy_loop['step_us_median']} us, "
+        f"{greedy_loop['distinct_tokens']} distinct tokens, same tokens on a second run")
 
     # --- per projection kind: 36 launches of one kind per replay ------------
     per_kernel = {}
@@ -744,6 +790,7 @@ def main() -> int:
             "persistent_us_per_step": {str(m): round(v * 1e3, 1) for m, v in sweep.items()},
             "step_with_rmsnorms_us": {str(m): v for m, v in norm_steps.items()},
             "decode_token_with_attention": {str(p): v for p, v in token_steps.items()},
+            "greedy_decode_loop": greedy_loop,
             "per_projection_m1": per_kernel,
             "lm_head_argmax": {str(m): v for m, v in head.items()},
             "prefill": {str(m): v for m, v in prefill.items()},

@@ -192,8 +192,9 @@ size_t lsk_attention_workspace_bytes(int n_q, int n_kv, int head_dim, int max_se
  *   out[n_q*d] = softmax(q K^T * scale) V over rows 0..pos, q head h reading
  *   kv head h / (n_q/n_kv), fp32 scores and softmax, bf16 output.
  * d must be 128, n_kv at most 64, n_q/n_kv one of 1, 2, 4, 8, and
- * max_seq_len at most 16384.  The pos+1 rows are split into at most 32
- * chunks of 128, 256, 384 or 512 rows (the smallest that fits), one
+ * max_seq_len at most 16384.  The pos+1 rows run as one chunk up to 128
+ * rows, as at most 8 chunks of 64 rows up to 512 rows, and beyond that as at
+ * most 32 chunks of 128, 256, 384 or 512 rows (the smallest that fits), one
  * workgroup each; with more than one chunk the partial results meet in
  * `workspace` (lsk_attention_workspace_bytes(), 256-byte aligned,
  * zero-filled before its first use; calls leave it zeroed; calls sharing one

@@ -2,8 +2,9 @@
 // o_proj projections of a Qwen3 decode layer, in one launch.
 //
 // Per (kv head j, chunk of the rows attended) one workgroup of 8 waves, from
-// the raw QKV projection row (chunks of 128, 256, 384 or 512 rows, the
-// smallest that keeps their count at 32 or below):
+// the raw QKV projection row (attention_rows_per_chunk: one chunk up to 128
+// rows, 64-row chunks up to 512 rows, then at most 32 chunks of 128, 256,
+// 384 or 512 rows):
 //   1. q heads jG..jG+G-1 and k head j: RMSNorm over head_dim with the q / k
 //      norm weights, then rotate-half RoPE with this position's cos / sin
 //      (src/leanstack/runtime/qwen_explicit.py:796-806, :690-716), in the
@@ -103,13 +104,16 @@ struct AttnArgs {
   unsigned* counters;      // workspace: one arrival counter per kv head
   unsigned char* partials; // workspace: one AttnPartial slot per (kv head, chunk)
   unsigned partial_bytes;  // bytes of all slots of this launch
-  int n_q, n_kv, s_max, pos, chunks;  // chunks of 128 * NU rows
+  int n_q, n_kv, s_max, pos, chunks;  // chunks of attention_rows_per_chunk(pos + 1) rows
   float eps, scale;
   int grid_chunks;                    // workgroups per kv head in the grid (>= chunks)
   const int* pos_ptr;                 // device-resident pos (then cos / sin are whole tables)
 };
 
 constexpr int kCoherent = 16;  // device-coherent buffer access (partials cross XCDs)
+// A buffer offset past every partial slot (num_records is at most 2^31 - 1):
+// the load returns zero without a memory access.
+constexpr unsigned kOutOfRange = 0x80000000u;
 constexpr unsigned kRawBufferDword3 = 0x00020000u;
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -122,8 +126,9 @@ __host__ __device__ constexpr unsigned partial_slot_bytes(int G) {
 // The last workgroup of kv head j: M_h = max_c m_c and
 // out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c, in chunk order.
 // Every partial value is requested in one round (NB * 8 chunk slots per
-// output, those past the last chunk re-read the last one and get weight 0),
-// together with the (m, l) pairs, so the combine waits for memory once.
+// output; those past the last chunk load from outside the buffer's range,
+// which returns zero and moves no data, and get weight 0), together with the
+// (m, l) pairs, so the combine waits for memory once.
 template <int G, int NB>
 __device__ __forceinline__ void combine_chunks(const AttnArgs& a, __amdgpu_buffer_rsrc_t parts, unsigned first,
                                                unsigned slot_bytes, int j, float (*mx)[G], float (*lsum)[G],
@@ -136,9 +141,12 @@ __device__ __forceinline__ void combine_chunks(const AttnArgs& a, __amdgpu_buffe
     const int e = min((int)threadIdx.x + o * kThreads, G * kHeadDim - 1);
 #pragma unroll
     for (int k = 0; k < kSlots; ++k) {
-      const unsigned kc = (unsigned)min(k, a.chunks - 1);
-      v[o][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, (unsigned)(2 * G + e) * 4u,
-                                                                              first + kc * slot_bytes, kCoherent));
+      // Out of range goes in the vector offset: the range check covers the
+      // vector and instruction offsets, not the scalar one.
+      const bool real = k < a.chunks;
+      const unsigned voff = (real ? 0u : kOutOfRange) + (unsigned)(2 * G + e) * 4u;
+      const unsigned base = real ? first + (unsigned)k * slot_bytes : 0u;
+      v[o][k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(parts, voff, base, kCoherent));
     }
   }
   // (m, l) of chunk k, head h, to thread kG + h; weights past the last
@@ -188,17 +196,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(AttnArgs arg
   constexpr int kRows = 16 * kWaves * NU;  // rows per workgroup at most: 128 NU
   constexpr int kMaxChunks = kAttnMaxChunks;
   AttnArgs a = args;
-  int rows = kRows;  // rows per chunk
   if constexpr (DYN) {
     const int pos = *args.pos_ptr;
     if (pos < 0 || pos >= a.s_max) return;
     a.pos = pos;
     a.cos += (size_t)pos * (kHeadDim / 2);
     a.sin += (size_t)pos * (kHeadDim / 2);
-    const int units = (pos + kAttnMinChunkRows) / kAttnMinChunkRows;  // ceil((pos + 1) / 128)
-    rows = kAttnMinChunkRows * ((units + kAttnMaxChunks - 1) / kAttnMaxChunks);
-    a.chunks = (pos + rows) / rows;  // ceil((pos + 1) / rows)
   }
+  // Rows per chunk (at most kRows: the launch picks NU for the largest chunk
+  // it can meet) and the chunk count, as the host computes them.
+  const int rows = attention_rows_per_chunk(a.pos + 1);
+  a.chunks = (a.pos + rows) / rows;  // ceil((pos + 1) / rows)
   const int j = blockIdx.x / a.grid_chunks;
   const int ci = blockIdx.x - j * a.grid_chunks;
   if (ci >= a.chunks) return;
@@ -513,16 +521,11 @@ hipError_t launch_g(const AttnArgs& a, int nu, hipStream_t stream) {
 
 }  // namespace
 
-int attention_chunk_rows(int rows) {
-  const int units = (rows + kAttnMinChunkRows - 1) / kAttnMinChunkRows;  // 128-row units
-  return kAttnMinChunkRows * ((units + kAttnMaxChunks - 1) / kAttnMaxChunks);
-}
+int attention_chunk_rows(int rows) { return attention_rows_per_chunk(rows); }
 
 size_t attention_workspace_bytes(int n_q, int n_kv, int max_seq_len) {
   const int group = n_q / n_kv;
-  const int most = (max_seq_len + kAttnMinChunkRows - 1) / kAttnMinChunkRows;
-  const size_t chunks = most < kAttnMaxChunks ? most : kAttnMaxChunks;
-  return kAttnPartialsOffset + (size_t)n_kv * chunks * partial_slot_bytes(group);
+  return kAttnPartialsOffset + (size_t)n_kv * attention_most_chunks(max_seq_len) * partial_slot_bytes(group);
 }
 
 namespace {
@@ -566,7 +569,7 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
                            workspace, ws_bytes);
   a.pos = pos;
   const int rows = attention_chunk_rows(pos + 1);
-  const int nu = rows / kAttnMinChunkRows;
+  const int nu = (rows + 127) / 128;  // 16-row groups per wave: 8 waves x 16 rows x nu cover the chunk
   a.chunks = (pos + 1 + rows - 1) / rows;
   a.grid_chunks = a.chunks;
   switch (n_q / n_kv) {
@@ -583,10 +586,7 @@ hipError_t launch_decode_attention(const void* qkv, int n_q, int n_kv, const voi
   }
 }
 
-int attention_grid_chunks(int max_seq_len) {
-  const int most = (max_seq_len + kAttnMinChunkRows - 1) / kAttnMinChunkRows;
-  return most < kAttnMaxChunks ? most : kAttnMaxChunks;
-}
+int attention_grid_chunks(int max_seq_len) { return attention_most_chunks(max_seq_len); }
 
 hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const void* q_norm_w, const void* k_norm_w,
                                       float eps, const void* cos_table, const void* sin_table, void* k_cache,
@@ -598,7 +598,7 @@ hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const 
   a.grid_chunks = attention_grid_chunks(s_max);
   // Chunks never exceed the size max_seq_len rows need (the rule grows with
   // the rows attended), so that size fixes the kernel's groups per wave.
-  const int nu = attention_chunk_rows(s_max) / kAttnMinChunkRows;
+  const int nu = (attention_chunk_rows(s_max) + 127) / 128;
   switch (n_q / n_kv) {
     case 1:
       return launch_dyn<1>(a, nu, stream);

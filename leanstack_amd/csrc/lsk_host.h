@@ -27,14 +27,41 @@ constexpr int kDecodeMaxM = 16;
 // multiple of 8).
 constexpr int kMaxActivationStride = (1 << 22) - 8;
 
-// Decode attention geometry (attention.hip): the rows attended are split into
-// at most kAttnMaxChunks chunks of a multiple of kAttnMinChunkRows rows.
+// Decode attention geometry (attention.hip): up to kAttnMinChunkRows rows
+// attended run as one chunk (one workgroup per kv head, no combine); up to
+// 8 * kAttnSplitRows rows as at most 8 chunks of kAttnSplitRows rows (one
+// combine round); beyond that, at most kAttnMaxChunks chunks of the smallest
+// multiple of kAttnMinChunkRows rows that allows it.
+#ifndef LSK_ATTN_SPLIT_ROWS
+#define LSK_ATTN_SPLIT_ROWS 64
+#endif
 constexpr int kAttnHeadDim = 128;
 constexpr int kAttnMinChunkRows = 128;
+constexpr int kAttnSplitRows = LSK_ATTN_SPLIT_ROWS;
 constexpr int kAttnMaxChunkRows = 512;
 constexpr int kAttnMaxChunks = 32;
 constexpr int kAttnMaxRows = kAttnMaxChunks * kAttnMaxChunkRows;  // 16384
 constexpr int kAttnMaxKvHeads = 64;
+static_assert(kAttnSplitRows % 16 == 0 && kAttnSplitRows >= 16 && kAttnSplitRows <= kAttnMinChunkRows,
+              "chunks are whole 16-row MFMA groups, at most one workgroup's 128");
+
+// Rows per chunk when `rows` rows (1..kAttnMaxRows) are attended; the host
+// and the kernel share it.
+constexpr int attention_rows_per_chunk(int rows) {
+  if (rows <= kAttnMinChunkRows) return kAttnMinChunkRows;
+  if (rows <= 8 * kAttnSplitRows) return kAttnSplitRows;
+  const int units = (rows + kAttnMinChunkRows - 1) / kAttnMinChunkRows;
+  return kAttnMinChunkRows * ((units + kAttnMaxChunks - 1) / kAttnMaxChunks);
+}
+
+// Chunk slots per kv head that a position below max_seq_len can need.
+constexpr int attention_most_chunks(int max_seq_len) {
+  if (max_seq_len <= kAttnMinChunkRows) return 1;
+  if (max_seq_len <= 8 * kAttnSplitRows) return (max_seq_len + kAttnSplitRows - 1) / kAttnSplitRows;
+  const int units = (max_seq_len + kAttnMinChunkRows - 1) / kAttnMinChunkRows;
+  const int most = units > 8 ? units : 8;
+  return most < kAttnMaxChunks ? most : kAttnMaxChunks;
+}
 
 // Record `fmt` as this thread's lsk_last_error() message; returns `status`.
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

@@ -130,15 +130,16 @@ hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void*
                                         const void* norm_w, float eps, void* y, int ldy, Epilogue epi,
                                         const void* residual, int ldr, hipStream_t stream);
 
-// Decode attention (attention.hip).  The rows attended are split into at
-// most kAttnMaxChunks chunks of the smallest multiple of kAttnMinChunkRows
-// that allows it (attention_chunk_rows), one workgroup per (kv head, chunk).
+// Decode attention (attention.hip).  The rows attended are split into
+// chunks by attention_rows_per_chunk (one chunk up to 128 rows, then at most
+// kAttnMaxChunks chunks of at least kAttnSplitRows rows), one workgroup per
+// (kv head, chunk).
 // Workspace: one arrival counter per kv head (kAttnMaxKvHeads words), then
 // from kAttnPartialsOffset one partial slot per (kv head, chunk).
 // Zero-filled before first use; every launch leaves the counters zero.
 constexpr size_t kAttnPartialsOffset = kAttnMaxKvHeads * 4;
 
-// Rows per chunk when `rows` rows are attended: 128, 256, 384 or 512.
+// Rows per chunk when `rows` rows are attended (attention_rows_per_chunk).
 int attention_chunk_rows(int rows);
 
 // Workspace bytes for n_kv kv heads of n_q / n_kv q heads and up to

@@ -195,13 +195,17 @@ __global__ __launch_bounds__(kNW * 64) void skinny_kernel(
       for (int b = 0; b < PB; ++b) {
         const int o = o0 + b;  // o-th other split in split order
         const int sp = o < split ? o : o + 1;
-        const unsigned base = o < S - 1 ? (unsigned)(grp * S + sp) * kSlot : 0x80000000u;
+        // Out of range goes in the vector offset: the range check covers the
+        // vector and instruction offsets, not the scalar one.
+        const bool real = o < S - 1;
+        const unsigned voff = (real ? 0u : 0x80000000u) + (unsigned)lane * 16u;
+        const unsigned base = real ? (unsigned)(grp * S + sp) * kSlot : 0u;
 #pragma unroll
         for (int r = 0; r < RBW; ++r)
 #pragma unroll
           for (int q = 0; q < MG; ++q)
             v[b][r][q] = __builtin_bit_cast(
-                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(parts, lane * 16, base + (r * MG + q) * 1024u, kCoherent));
+                f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(parts, voff, base + (r * MG + q) * 1024u, kCoherent));
       }
 #pragma unroll
       for (int b = 0; b < PB; ++b) {

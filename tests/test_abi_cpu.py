@@ -138,13 +138,21 @@ def test_decode_attention_at_rejects_before_launch(kwargs, code):
 
 def test_attention_workspace_bytes():
     """Counters for 64 kv heads, then one (m, l, acc) slot of 4 * (2G + 128G)
-    bytes per (kv head, chunk); at most 32 chunks of at least 128 rows."""
+    bytes per (kv head, chunk) for the most chunks a position below
+    max_seq_len needs: 1 up to 128 rows, 64-row chunks up to 512 rows (at
+    most 8), then chunks of a multiple of 128 rows (at most 32)."""
     lib = _lib.load()
     slot = 4 * (2 * 4 + 128 * 4)
     assert lib.lsk_attention_workspace_bytes(32, 8, 128, 4096) == 256 + 8 * 32 * slot
     assert lib.lsk_attention_workspace_bytes(32, 8, 128, 16384) == 256 + 8 * 32 * slot
     assert lib.lsk_attention_workspace_bytes(32, 8, 128, 1000) == 256 + 8 * 8 * slot
     assert lib.lsk_attention_workspace_bytes(32, 8, 128, 100) == 256 + 8 * 1 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 128) == 256 + 8 * 1 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 129) == 256 + 8 * 3 * slot   # 3 chunks of 64 rows
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 300) == 256 + 8 * 5 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 512) == 256 + 8 * 8 * slot
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 600) == 256 + 8 * 8 * slot   # 512 rows need 8
+    assert lib.lsk_attention_workspace_bytes(32, 8, 128, 1500) == 256 + 8 * 12 * slot
     assert lib.lsk_attention_workspace_bytes(32, 8, 64, 4096) == 0      # head_dim
     assert lib.lsk_attention_workspace_bytes(24, 8, 128, 4096) == 0     # 3 q heads per kv head
     assert lib.lsk_attention_workspace_bytes(32, 8, 128, 16385) == 0    # too many rows

@@ -65,12 +65,14 @@ def _check_case(n_q, n_kv, s_max, pos, seed):
     assert (kdiff <= k2[:, pos].float().abs() * 2.0 ** -7 + 1e-30).all(), f"{what}: k row beyond one bf16 step"
 
 
-@pytest.mark.parametrize("pos", [0, 1, 2, 15, 16, 17, 63, 64, 127, 128, 319, 511, 512, 513, 1000, 1023, 1024,
-                                 2047, 3071, 3072, 4095])
+@pytest.mark.parametrize("pos", [0, 1, 2, 15, 16, 17, 63, 64, 127, 128, 191, 192, 319, 511, 512, 513, 1000, 1023,
+                                 1024, 1500, 2047, 3071, 3072, 4095])
 def test_decode_attention_qwen3_4b(gpu, pos):
     """32 q heads, 8 kv heads, head_dim 128, a 4096-row cache: one 128-row
-    chunk up to pos 127, then 2..32 chunks combined through the workspace
-    (8, 16, 24 and 32 chunk slots per combine round at the edges)."""
+    chunk up to pos 127, 3..8 chunks of 64 rows up to pos 511 (the last one
+    holding 1 or 64 rows), then 5..32 chunks of 128 rows combined through the
+    workspace (8, 16, 24 and 32 chunk slots per combine round at the edges;
+    pos 1500: 12 chunks, so 4 slots of the round lie past the last chunk)."""
     _check_case(G.num_attention_heads, G.num_key_value_heads, 4096, pos, seed=9000 + pos)
 
 
@@ -117,7 +119,7 @@ def _device_pos_case(s_max, positions, seed):
 
 def test_decode_attention_device_position(gpu):
     """Positions in device memory at every chunk-rule regime up to 4096 rows."""
-    _device_pos_case(4096, [0, 1, 127, 128, 129, 511, 1000, 2047, 3072, 4095], 9400)
+    _device_pos_case(4096, [0, 1, 127, 128, 129, 200, 511, 512, 1000, 1500, 2047, 3072, 4095], 9400)
 
 
 def test_decode_attention_device_position_long_cache(gpu):
