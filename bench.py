@@ -12,8 +12,9 @@ activations read + outputs written) / step time, in GB/s.
 Also reported (under "detail"): the verify sweep M = 1, 2, 4, 8 over the same
 stack, the step with the two RMSNorms of each layer (fused into the QKV and
 gate_up kernels, or as separate F.rms_norm launches), a whole decode token with
-attention over 320 and 4095 cached rows (every layer HIP), a greedy decode loop of
-256 tokens (one graph replay per token, per-step events), each projection kind's
+attention over 320 and 4095 cached rows (every layer HIP), a greedy decode loop in
+the reference's decode_64_256 shape (256 tokens after 64 cached rows, one graph
+replay per token, per-step events), each projection kind's
 per-launch time, the tied lm_head + argmax at M = 1..8, and the prefill GEMMs
 at M = 512, 2048, 8192 in TFLOP/s.
 
@@ -585,13 +586,15 @@ def main() -> int:
 
     # --- a greedy decode loop: each token the argmax of the one before -------
     # The reference's decode loop (qwen_explicit_runtime_loop.py:331-385) with
-    # its per-step events: here one graph of DecodeStep.launch_next (embedding
+    # its per-step events, in the shape of its decode_64_256 benchmark (a
+    # 64-token prompt, 256 generated tokens): the cache rows below position
+    # 64 stand for the prompt.  One graph of DecodeStep.launch_next (embedding
     # row of the last token, the 36 layers, the head, token record, position
     # advance) is replayed once per token, with a pair of events around each
     # replay and one pair around the loop. The loop runs twice from the same
     # start (same first token, position and cache rows below it): the second
     # run must emit the same tokens.
-    loop_tokens, loop_start = 256, 320
+    loop_tokens, loop_start = 256, 64
     embedding = (0.02 * torch.randn((G.vocab_size, G.hidden_size), generator=gen, device=dev)).to(torch.bfloat16)
     emitted = torch.full((kv_rows,), -1, device=dev, dtype=torch.long)
     graph = stack.capture(lambda: token_step.launch_next(embedding, emitted))
@@ -618,6 +621,7 @@ def main() -> int:
     if not torch.equal(runs[0][2], toks) or int(toks.min()) < 0:
         raise SystemExit("greedy decode loop: the two runs from the same start emitted different tokens")
     greedy_loop = {
+        "workload": "decode_64_256 shape: 64 cached prompt rows, 256 greedy tokens (prefill not timed)",
         "tokens": loop_tokens, "first_position": loop_start, "loop_us": round(loop_us, 1),
         "tokens_per_s": round(loop_tokens / (loop_us * 1e-6), 1),
         "step_us_median": round(step_us[len(step_us) // 2], 1), "step_us_p10": round(step_us[len(step_us) // 10], 1),
@@ -661,24 +665,28 @@ def main() -> int:
     logits = torch.empty((16, G.vocab_size), device=dev, dtype=torch.float32)
     ws = kernels.LmHeadWorkspace(16, G.vocab_size, G.hidden_size, dev)
     tokens = torch.empty((16,), device=dev, dtype=torch.long)
+    # The greedy head as the reference's cuTile head runs it (fp32 scores,
+    # tile maxima, argmax; no logits written: cutile_logits.py:17-31, :67-69),
     # 4 calls per graph replay (as the prefill GEMMs run 8), so that one
-    # replay's own launch cost is not charged to one call; the figure with one
-    # call per replay is reported beside it.
+    # replay's own launch cost is not charged to one call.  Beside it: one
+    # call per replay, and the same head also writing the fp32 logits.
     head_reps = 4
     for m in (1, 2, 4, 8):
-        def head_fn(m=m, reps=head_reps):
+        def head_fn(m=m, reps=head_reps, with_logits=False):
             for _ in range(reps):
-                kernels.lm_head_argmax(hidden[:m], lm_head, logits_out=logits[:m], workspace=ws, out=tokens[:m])
-        graph = stack.capture(head_fn)
-        ms = time_graph(torch, graph, steps, warmup) / head_reps
-        del graph
-        graph = stack.capture(lambda m=m: head_fn(m, 1))
-        ms1 = time_graph(torch, graph, steps, warmup)
-        del graph
-        head[m] = {"us": round(ms * 1e3, 2), "GB/s": round(G.lm_head_call_bytes(m) / (ms * 1e-3) / 1e9, 1),
-                   "us_one_call_per_replay": round(ms1 * 1e3, 2)}
-        log(f"lm_head M={m}: {head[m]['us']} us ({head[m]['us_one_call_per_replay']} us as one call per replay), "
-            f"{head[m]['GB/s']} GB/s")
+                kernels.lm_head_argmax(hidden[:m], lm_head, logits_out=logits[:m] if with_logits else None,
+                                       workspace=ws, out=tokens[:m])
+        row = {}
+        for key, fn, reps in (("us", head_fn, head_reps), ("us_one_call_per_replay", lambda m=m: head_fn(m, 1), 1),
+                              ("us_with_fp32_logits", lambda m=m: head_fn(m, head_reps, True), head_reps)):
+            graph = stack.capture(fn)
+            settle(torch, graph, 0.05)
+            row[key] = round(time_graph(torch, graph, steps, warmup) / reps * 1e3, 2)
+            del graph
+        row["GB/s"] = round(G.lm_head_call_bytes(m, logits=False) / (row["us"] * 1e-6) / 1e9, 1)
+        head[m] = row
+        log(f"lm_head M={m}: {row['us']} us ({row['us_one_call_per_replay']} us as one call per replay, "
+            f"{row['us_with_fp32_logits']} us also writing fp32 logits), {row['GB/s']} GB/s")
 
     # --- prefill GEMMs ---------------------------------------------------------
     prefill = {}

@@ -74,9 +74,13 @@ class QwenGeometry:
     def stack_bytes(self, m: int) -> int:
         return self.num_hidden_layers * self.layer_bytes(m)
 
-    def lm_head_call_bytes(self, m: int) -> int:
-        """Weights + hidden rows (bf16) + fp32 logits (the cuTile head's score precision)."""
-        return self.lm_head_bytes() + m * self.hidden_size * BF16_BYTES + m * self.vocab_size * 4
+    def lm_head_call_bytes(self, m: int, logits: bool = True) -> int:
+        """Weights + hidden rows (bf16), + fp32 logits when the call writes
+        them (the cuTile head's score precision).  The greedy head of the
+        reference (cutile_logits.py:17-31) writes only its tile maxima, so
+        its bytes are the weights and hidden rows (logits=False)."""
+        return (self.lm_head_bytes() + m * self.hidden_size * BF16_BYTES
+                + (m * self.vocab_size * 4 if logits else 0))
 
     def projection_flops(self, name: str, m: int) -> int:
         n, k = self.projections()[name]

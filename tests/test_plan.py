@@ -44,6 +44,7 @@ def test_per_step_byte_accounting():
     assert G.stack_bytes(8) == 7_289_634_816
     assert G.lm_head_bytes() == 777_912_320
     assert G.lm_head_call_bytes(1) == 777_912_320 + 5_120 + 607_744
+    assert G.lm_head_call_bytes(1, logits=False) == 777_912_320 + 5_120
     assert G.layer_flops(2048) == 2 * 2048 * G.layer_params()
     assert round(G.layer_flops(2048) / 1e9, 2) == 413.39
 
