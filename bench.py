@@ -171,12 +171,12 @@ def cpu_baseline(g, seconds: float) -> dict:
     }
 
 
-def cpu_gemv_config1(seconds: float) -> dict:
-    """Config 1: the o_proj GEMV x[1,4096] . W[2560,4096]^T on the CPU torch
+def cpu_o_proj_gemv(seconds: float) -> dict:
+    """The o_proj GEMV x[1,4096] . W[2560,4096]^T alone on the CPU torch
     path (torch.mv in bf16, qwen_explicit.py:913 via the oracle), W ~
     N(0,0.02), x ~ N(0,1), seeded, timed for about `seconds` on this host's
     cores.  W is 21 MB, so on a host with a large L3 the repeated calls may
-    read it from cache; that is the configuration as stated."""
+    read it from cache; that is the workload as stated."""
     import torch
 
     from oracle import projections as ref
@@ -402,7 +402,7 @@ def main() -> int:
                          "M = 512, 2048 and 8192, three launches each, no graphs")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+        print(json.dumps({"error": "this benchmark runs on one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}), flush=True)
         return 2
 
@@ -744,9 +744,9 @@ def main() -> int:
     if not args.quick:
         cpu = cpu_baseline(G, args.cpu_seconds)
         log(f"cpu baseline: {cpu['value']} GB/s on {cpu['cores']} threads")
-        cpu["config1_o_proj_gemv"] = cpu_gemv_config1(min(3.0, args.cpu_seconds))
-        log(f"cpu baseline, config 1 o_proj GEMV: {cpu['config1_o_proj_gemv']['us']} us, "
-            f"{cpu['config1_o_proj_gemv']['GB/s']} GB/s")
+        cpu["o_proj_gemv_2560x4096"] = cpu_o_proj_gemv(min(3.0, args.cpu_seconds))
+        log(f"cpu baseline, o_proj GEMV 2560x4096 at M=1 alone: {cpu['o_proj_gemv_2560x4096']['us']} us, "
+            f"{cpu['o_proj_gemv_2560x4096']['GB/s']} GB/s")
 
     result = {
         "metric": METRIC,

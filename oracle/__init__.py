@@ -1,7 +1,7 @@
 """CPU oracle of the BF16 projection path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this package, and only as the checker (or as the timed CPU baseline).  The
+this package, and only to check results (or as the timed CPU baseline).  The
 product path (leanstack_amd) never imports it and has no CPU fallback.
 
 Modules

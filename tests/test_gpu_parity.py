@@ -98,7 +98,7 @@ def test_auto_workspaces_are_per_stream(gpu):
     assert kernels.prefill_workspace(dev, 2048, 2560, 4096).data_ptr() == a.data_ptr()
 
 
-def test_o_proj_gemv_config1(gpu):
+def test_o_proj_gemv_2560x4096(gpu):
     """x[1,4096] ~ N(0,1), W[2560,4096] ~ N(0,0.02): elementwise within bf16
     rounding + the fp32 summation bound of the float64 brute force."""
     w = weight(2560, 4096, seed=0)
