@@ -275,7 +275,8 @@ int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, 
  * time), so the call allocates nothing.  No counterpart in the reference; it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Limit:
- * 64 + M * (V / 32) * 8 bytes must fit in 1 MiB (every M <= 16 at
+ * 64 + M * P * 8 bytes, P = (V/16 - 512) / 2 + 512 (the scoring
+ * workgroups), must fit in 1 MiB (every M <= 16 at
  * V = 151936); larger calls return LSK_ERR_INVALID before anything touches
  * the GPU.  All calls on one
  * device share the array: calls that overlap in time on a device (streams not

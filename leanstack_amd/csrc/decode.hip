@@ -691,61 +691,47 @@ __device__ __forceinline__ void reduce_row_partials(ArgmaxPartial* __restrict__ 
   }
 }
 
-// lm_head scores for RBW row-blocks (vocab rows) + the argmax, in one launch.
-// Grid: P = NB / RBW scoring workgroups, then M reducing ones.  Scoring
-// workgroup b stores partial[m * P + b] = its best (score, index) for row m;
-// reducing workgroup P + m -- dispatched after every scoring one, so it waits
-// only for workgroups that are running or done -- reduces row m into
-// out_idx[m] while the last scoring workgroups finish (reduce_row_partials).
-// The workspace must be zero when a call starts, and every call leaves it
-// zero.
+// lm_head scores for RB row-blocks (vocab rows) from row-block rb0, and their
+// best (score, index) per activation row stored as partial[m * P + slot].
 // NC > 0: the activations staged through LDS (NC chunks per lane), or with
 // NORM their RMSNorm (norm_w, eps) applied on the way (the dense prologue).
-template <int NW, int RBW, int U, int NC = 0, bool NORM = false>
-__global__ __launch_bounds__(NW * 64) void lm_head_kernel(
-    const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, float* __restrict__ logits,
-    int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, unsigned* __restrict__ status,
-    long long* __restrict__ out_idx, int M, int KT, const __bf16* __restrict__ norm_w, float eps) {
-  static_assert(!NORM || NC > 0, "the RMSNorm prologue is the dense single-round one");
-  const int P = (int)gridDim.x - M;
-  if ((int)blockIdx.x >= P) {
-    const int row = (int)blockIdx.x - P;
-    reduce_row_partials<NW * 64>(partial + (size_t)row * P, P, out_idx + row, status);
-    return;
-  }
+template <int NW, int RB, int U, int NC, bool NORM>
+__device__ __forceinline__ void lm_head_score(const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx,
+                                              float* __restrict__ logits, int V, int logits_bf16,
+                                              ArgmaxPartial* __restrict__ partial, int P, int M, int KT,
+                                              const __bf16* __restrict__ norm_w, float eps, int rb0, int slot) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m = lane & 15;
   const int g = lane >> 4;
   const bool m_active = m < M;
-  const int rb0 = blockIdx.x * RBW;
   const int kb = (KT * wave) / NW;
   const int ke = (KT * (wave + 1)) / NW;
 
-  f32x4_t acc[RBW];
+  f32x4_t acc[RB];
 #pragma unroll
-  for (int r = 0; r < RBW; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < RB; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const bf16x8_t* xrow = reinterpret_cast<const bf16x8_t*>(x + (size_t)(m_active ? m : 0) * ldx) + g;
   const bf16x8_t* wt = w + (size_t)rb0 * KT * 64 + lane;
   bool leader;  // wave 0, which holds the sums after reduce_waves
   if constexpr (NORM) {
     (void)xrow;
     (void)ke;
-    accumulate_rows_rms_dense<NW, RBW, U, NC>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w), M, KT,
+    accumulate_rows_rms_dense<NW, RB, U, NC>(acc, wt, x, ldx, reinterpret_cast<const bf16x8_t*>(norm_w), M, KT,
                                               kb, wave, lane, eps);
-    leader = reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NC, M, RBW));
+    leader = reduce_waves_at<NW, RB>(acc, wave, lane, rms_lds, rms_wave_bytes(U, NC, M, RB));
   } else if constexpr (NC > 0) {  // activations staged through LDS, NC chunks per lane
     (void)xrow;
     (void)ke;
     (void)norm_w;
     (void)eps;
-    accumulate_rows_staged<NW, RBW, U, NC, false>(acc, wt, x, ldx, M, KT, kb, wave, lane);
-    leader = reduce_waves_at<NW, RBW>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RBW));
+    accumulate_rows_staged<NW, RB, U, NC, false>(acc, wt, x, ldx, M, KT, kb, wave, lane);
+    leader = reduce_waves_at<NW, RB>(acc, wave, lane, rms_lds, staged_wave_bytes(U, M, RB));
   } else {
     (void)norm_w;
     (void)eps;
-    accumulate_rows<RBW, U>(acc, wt, xrow, m_active, KT, kb, ke);
-    leader = reduce_waves<NW, RBW>(acc, wave, lane);
+    accumulate_rows<RB, U>(acc, wt, xrow, m_active, KT, kb, ke);
+    leader = reduce_waves<NW, RB>(acc, wave, lane);
   }
 
   if (leader) {
@@ -754,7 +740,7 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
     float best = -__builtin_huge_valf();
     int best_idx = INT_MAX;
 #pragma unroll
-    for (int r = 0; r < RBW; ++r) {
+    for (int r = 0; r < RB; ++r) {
       const int n0 = (rb0 + r) * 16 + 4 * g;
       f32x4_t s = acc[r];
       if (logits_bf16) {
@@ -772,7 +758,44 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
       const int oi = __shfl_xor(best_idx, off);
       argmax_take(best, best_idx, os, oi);
     }
-    if (g == 0 && m_active) store_partial(partial + (size_t)m * P + blockIdx.x, best, best_idx);
+    if (g == 0 && m_active) store_partial(partial + (size_t)m * P + slot, best, best_idx);
+  }
+}
+
+// lm_head scores + the argmax, in one launch.  Grid: P scoring workgroups,
+// then M reducing ones (lm_head_partials).  The first P2 scoring workgroups
+// take RBW row-blocks each and the last P - P2 one each, so that the grid's
+// last workgroups are short and finish close together (the CUs otherwise
+// idle through the end of the last long ones); NB = RBW * P2 + (P - P2).
+// Scoring workgroup b stores partial[m * P + b] = its best (score, index)
+// for row m; reducing workgroup P + m -- dispatched after every scoring one,
+// so it waits only for workgroups that are running or done -- reduces row m
+// into out_idx[m] while the last scoring workgroups finish
+// (reduce_row_partials).  The workspace must be zero when a call starts, and
+// every call leaves it zero.
+template <int NW, int RBW, int U, int NC = 0, bool NORM = false>
+__global__ __launch_bounds__(NW * 64) void lm_head_kernel(
+    const bf16x8_t* __restrict__ w, const __bf16* __restrict__ x, int ldx, float* __restrict__ logits,
+    int V, int logits_bf16, ArgmaxPartial* __restrict__ partial, unsigned* __restrict__ status,
+    long long* __restrict__ out_idx, int M, int KT, const __bf16* __restrict__ norm_w, float eps) {
+  static_assert(!NORM || NC > 0, "the RMSNorm prologue is the dense single-round one");
+  const int P = (int)gridDim.x - M;
+  const int b = (int)blockIdx.x;
+  if (b >= P) {
+    const int row = b - P;
+    reduce_row_partials<NW * 64>(partial + (size_t)row * P, P, out_idx + row, status);
+    return;
+  }
+  if constexpr (RBW == 1) {
+    lm_head_score<NW, 1, U, NC, NORM>(w, x, ldx, logits, V, logits_bf16, partial, P, M, KT, norm_w, eps, b, b);
+  } else {
+    const int P2 = (V / kTileRows - P) / (RBW - 1);
+    if (b < P2)
+      lm_head_score<NW, RBW, U, NC, NORM>(w, x, ldx, logits, V, logits_bf16, partial, P, M, KT, norm_w, eps,
+                                          b * RBW, b);
+    else
+      lm_head_score<NW, 1, U, NC, NORM>(w, x, ldx, logits, V, logits_bf16, partial, P, M, KT, norm_w, eps,
+                                        P2 * RBW + (b - P2), b);
   }
 }
 
@@ -1082,14 +1105,23 @@ hipError_t launch_decode_rmsnorm_linear(const void* w, int N, int K, const void*
   return launch_decode_epi<true>(a, epi, stream);
 }
 
-int lm_head_partials(int V) { return (V / kTileRows) / kLmHeadRBW; }
+// Single-row-block workgroups at the end of the lm_head grid: 2 per CU of a
+// 256-CU MI355X (measured at V = 151936, M = 1: 115.1 -> 113.9 us; a tail of
+// 384, 768 or 1024 was no better).
+constexpr int kLmHeadTail = 512;
+
+int lm_head_partials(int V) {
+  const int NB = V / kTileRows;
+  if (kLmHeadRBW == 1 || NB <= kLmHeadTail) return NB;
+  const int tail = kLmHeadTail + (NB - kLmHeadTail) % kLmHeadRBW;  // NB - tail: whole RBW groups
+  return (NB - tail) / kLmHeadRBW + tail;
+}
 
 hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int M, int ldx, float* logits,
                                  int logits_bf16, long long* out_idx, void* workspace,
                                  const void* norm_w, float eps, hipStream_t stream) {
-  const int NB = V / kTileRows;
   const int KT = K / kTileK;
-  const int P = NB / kLmHeadRBW;
+  const int P = lm_head_partials(V);
   auto* status = static_cast<unsigned*>(workspace);
   auto* partials = reinterpret_cast<ArgmaxPartial*>(static_cast<unsigned char*>(workspace) + kLmHeadStatusBytes);
   const auto* nw = static_cast<const __bf16*>(norm_w);

@@ -6,8 +6,9 @@
 // device array, instead of a caller-allocated one.  For callers that cannot
 // allocate device memory: code under HIP graph capture, tight serving loops.
 //
-// Limits and sharing: one call's workspace takes 64 + M * (V / 32) * 8
-// bytes, at most kScratchBytes (1 MiB: every M <= 16 at V = 151936); larger
+// Limits and sharing: one call's workspace takes 64 + M * P * 8 bytes (P
+// scoring workgroups: (V/16 - 512) / 2 + 512 for V/16 > 512, else V/16), at
+// most kScratchBytes (1 MiB: every M <= 16 at V = 151936); larger
 // calls are rejected before anything touches the GPU.  The array starts
 // zeroed (a device global without an initializer) and every call leaves its
 // partials zero again, which is the state the kernel needs, so nothing is
@@ -61,7 +62,7 @@ extern "C" int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_
   if (need > kScratchBytes) {
     return lsk::fail(LSK_ERR_INVALID,
                      "M=%d rows over V=%d need %zu bytes of argmax workspace; the static scratch holds %zu "
-                     "(64 + M * V / 32 * 8 bytes at most): use lsk_lm_head_argmax_bf16 with a workspace",
+                     "(64 + M * P * 8 bytes, P = (V/16 - 512) / 2 + 512): use lsk_lm_head_argmax_bf16 with a workspace",
                      M, V, need, kScratchBytes);
   }
   int device = 0;

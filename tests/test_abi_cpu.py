@@ -162,7 +162,9 @@ def test_lm_head_rejects_before_launch():
     lib = _lib.load()
     ok = dict(V=151936, K=2560, M=1)
     ws = lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 1, 151936, 2560)
-    assert ws == 64 + (151936 // 32) * 8  # status header + one partial per 32 vocab rows
+    # status header + one partial per scoring workgroup: 4492 of two 16-row
+    # vocab blocks, then a tail of 512 single blocks (151936 / 16 = 9496 = 2 * 4492 + 512)
+    assert ws == 64 + (4492 + 512) * 8
     cases = [
         (dict(M=17), _lib.ERR_INVALID),
         (dict(V=151920), _lib.ERR_INVALID),   # V % 32 != 0
@@ -288,8 +290,8 @@ def test_launch_next_refuses_a_bad_token_buffer():
 
 def test_noalloc_lm_head_rejects_before_launch():
     """The allocation-free head refuses calls whose workspace exceeds its
-    static scratch (64 + M * V / 32 * 8 bytes > 1 MiB) and the usual bad
-    arguments, before touching the GPU."""
+    static scratch (64 + M * P * 8 bytes > 1 MiB, P = (V/16 - 512) / 2 + 512
+    scoring workgroups) and the usual bad arguments, before touching the GPU."""
     lib = _lib.load()
 
     def call(**over):
@@ -298,9 +300,9 @@ def test_noalloc_lm_head_rejects_before_launch():
         return lib.lsk_lm_head_argmax_noalloc_bf16(a["w"], a["layout"], a["v"], a["k"], a["x"], a["m"], a["ldx"],
                                                    a["logits"], a["mode"], a["out"], None)
 
-    st = call(m=16, v=1 << 19)  # 16 rows x 16384 partials x 8 B = 2 MiB
+    st = call(m=16, v=1 << 19)  # 16 rows x 16640 partials x 8 B = 2.03 MiB
     assert st == _lib.ERR_INVALID and "static scratch" in _lib.last_error()
-    st = call(m=16, v=1 << 18)  # partials fill exactly 1 MiB: the status header is 64 bytes over
+    st = call(m=16, v=253952)  # P = 8192: the partials fill exactly 1 MiB, the status header is 64 bytes over
     assert st == _lib.ERR_INVALID and "static scratch" in _lib.last_error()
     assert call(m=17) == _lib.ERR_INVALID
     assert call(layout=2) == _lib.ERR_LAYOUT
