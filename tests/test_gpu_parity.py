@@ -116,9 +116,10 @@ def test_o_proj_gemv_2560x4096(gpu):
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16])
 def test_decode_projection(gpu, name, m):
     """Every M of the decode forms: the staged-activation kernels switch their
-    chunks per lane with M (QKV 1..5 up to M = 8, o_proj 1..6 up to M = 6,
-    down 2..4 up to M = 3), then fragment loads per tile; M = 9..15 leave
-    part of the 16 MFMA columns unused."""
+    chunks per lane with M (QKV 1..5 up to M = 8, o_proj 1..8 up to M = 8,
+    down 2..6 up to M = 5, then two phases of 4 or 5 at M = 6..8), then
+    fragment loads per tile; M = 9..15 leave part of the 16 MFMA columns
+    unused."""
     n, k = PROJ[name]
     w = weight(n, k, seed=10 + m)
     x = activations(m, k, seed=100 + m)
@@ -404,6 +405,37 @@ def test_lm_head_ties_pick_lowest_index(gpu):
     for mode in (_lib.LOGITS_FP32, _lib.LOGITS_BF16):
         idx = kernels.lm_head_argmax(h.to(dev), pw, logits_mode=mode).cpu()
         assert idx.tolist() == [1234]
+
+
+@pytest.mark.parametrize("v", [16 * 512, 16 * 514, 16 * 2048])
+def test_lm_head_tail_workgroups(gpu, v):
+    """The scoring grid takes two 16-row vocab blocks per workgroup, then a
+    tail of 512 one-block workgroups (all one-block up to 512 blocks): at
+    512, 514 and 2048 blocks every row's fp32 score equals the CPU's (each
+    row scored once, in its own place), and a maximum planted in the first
+    and last pair, the first and last tail block and the last row is found."""
+    k = 256
+    dev = torch.device("cuda:0")
+    h = activations(1, k, seed=740)
+    hot = torch.sign(h.float()).to(torch.bfloat16) * 0.5
+    nb = v // 16
+    pairs = (nb - 512) // 2 if nb > 512 else 0
+    tail0 = 32 * pairs  # first vocab row of the tail
+    rows = sorted({0, 31, max(tail0 - 1, 0), tail0, tail0 + 16, v - 17, v - 1})
+    for row in rows:
+        e = weight(v, k, seed=741)
+        e[row] = hot
+        pw = PackedWeight.from_rowmajor(e.to(dev))
+        logits = torch.empty((1, v), device=dev, dtype=torch.float32)
+        idx = kernels.lm_head_argmax(h.to(dev), pw, logits_out=logits).cpu()
+        assert idx.tolist() == [row], (v, row, idx.tolist())
+        if row == rows[0]:
+            expect = ref.logits_scores_fp32(h, e)
+            got = logits.cpu()
+            assert_parity(got, expect, f"lm_head logits V={v}")
+            # elementwise: fp32 sums of 256 products in another order, far below one misplaced row
+            err = (got - expect).abs().max()
+            assert float(err) <= 1e-4 * float(expect.abs().max()) + 1e-5, (v, float(err))
 
 
 def test_device_pack_matches_host_packer(gpu):
