@@ -1011,7 +1011,8 @@ hipError_t launch_decode_shape(const DecodeArgs& a, hipStream_t stream) {
   // Activations staged through LDS (staged_x(NC), NC = chunks per lane of
   // the wave's M * 4 * k-tiles chunks) wherever the registers allow: QKV and
   // o_proj for every M <= 8, gate_up (4 waves x 10 pairs up to M = 2, then
-  // 8 waves x 5), down up to M = 6 (its 16 waves then hold 118 KB of LDS).
+  // 8 waves x 5), down in one phase up to M = 5 and in two from M = 6 (its
+  // 16 waves hold up to 154 KB of LDS at M = 8).
   if (a.KT == 80 && a.M <= 8) {
     if constexpr (RBW == 1) return launch_staged<8, RBW, EPI, 5, true>(a, (40 * a.M + 63) / 64, stream);
     if constexpr (RBW == 2) {
