@@ -252,10 +252,12 @@ def probe_step_floor(torch, steps: int, warmup: int) -> dict:
     {qkv, o, gate_up, down}, each CU streaming an equal share of each
     projection, every tile multiplied, nothing else computed): one
     persistent launch with no dependency between projections, with a flat
-    grid barrier before each, with the two-level barrier; and a HIP graph of
-    144 single-projection launches of the same kernel (the structure of the
-    product step).  Each launch timed with events on its stream, median of
-    `steps` after `warmup`."""
+    grid barrier before each, with the two-level barrier, with tag words;
+    the same dependency forms on 144 segments of 12 KB per CU (the
+    boundary's own latency); and a HIP graph of 144 single-projection
+    launches of the same kernel (the structure of the product step).  Each
+    launch timed with events on its stream, median of `steps` after
+    `warmup`."""
     import ctypes
 
     from leanstack_amd import _lib
@@ -293,15 +295,37 @@ def probe_step_floor(torch, steps: int, warmup: int) -> dict:
         return statistics.median(out)
 
     res = {"bytes": total, "projections": len(seg), "cus": cus}
-    for name, mode, ring in (("one_launch_no_dependency_ring4", 0, 4), ("one_launch_no_dependency_ring16", 0, 16),
-                             ("one_launch_flat_barrier_ring4", 1, 4), ("one_launch_two_level_barrier_ring4", 2, 4),
-                             ("one_launch_two_level_barrier_ring16", 2, 16)):
+    forms = [("one_launch_no_dependency_ring4", 0, 4), ("one_launch_no_dependency_ring16", 0, 16),
+             ("one_launch_flat_barrier_ring4", 1, 4), ("one_launch_two_level_barrier_ring4", 2, 4),
+             ("one_launch_two_level_barrier_ring16", 2, 16)]
+    if cus <= 256:  # the tag-word form holds one word per CU for at most 256 CUs
+        forms.append(("one_launch_tag_words_ring4", 3, 4))
+    for name, mode, ring in forms:
         us = timed(lambda: launch(mode, ring))
         torch.cuda.synchronize()
         if int(ws[:4].view(torch.int32).item()) != 0:
             raise SystemExit(f"probe {name}: a bounded wait gave up")
         res[name] = {"us": round(us, 1), "GB/s": round(total / (us * 1e-6) / 1e9, 1)}
         log(f"probe {name}: {us:.1f} us, {total / (us * 1e-6) / 1e9:.0f} GB/s")
+    # The boundary's own latency: 144 segments of one tile per compute wave
+    # (12 KB per CU), so each segment streams in well under a microsecond and
+    # the launch is almost all boundaries.
+    small = [cus * 12] * len(seg)
+    small_arr = (ctypes.c_longlong * len(small))(*small)
+    lat = {}
+    for name, mode in (("no_dependency", 0), ("two_level_barrier", 2), ("tag_words", 3)):
+        if mode == 3 and cus > 256:
+            continue
+        us = timed(lambda: launch(mode, 4, segs=small_arr, count=len(small), nbytes=sum(small) * 1024))
+        torch.cuda.synchronize()
+        if int(ws[:4].view(torch.int32).item()) != 0:
+            raise SystemExit(f"probe {name} on 12 KB segments: a bounded wait gave up")
+        lat[name] = {"us": round(us, 1)}
+        log(f"probe {name} on 12 KB segments: {us:.1f} us")
+    for name in lat:
+        if name != "no_dependency":
+            lat[name]["us_per_boundary"] = round((lat[name]["us"] - lat["no_dependency"]["us"]) / (len(small) - 1), 2)
+    res["segments_of_12_tiles_per_cu"] = lat
     # 144 dependent launches, one projection each, captured as one graph
     offsets, off = [], 0
     singles = []
@@ -328,8 +352,9 @@ def probe_step_floor(torch, steps: int, warmup: int) -> dict:
     log(f"probe graph of 144 launches: {us:.1f} us, {total / (us * 1e-6) / 1e9:.0f} GB/s")
     base = res["one_launch_no_dependency_ring4"]["us"]
     for name in ("one_launch_flat_barrier_ring4", "one_launch_two_level_barrier_ring4",
-                 "one_launch_two_level_barrier_ring16", "graph_of_144_launches_ring4"):
-        res[name]["us_per_boundary_over_no_dependency"] = round((res[name]["us"] - base) / (len(seg) - 1), 2)
+                 "one_launch_two_level_barrier_ring16", "one_launch_tag_words_ring4", "graph_of_144_launches_ring4"):
+        if name in res:
+            res[name]["us_per_boundary_over_no_dependency"] = round((res[name]["us"] - base) / (len(seg) - 1), 2)
     return res
 
 

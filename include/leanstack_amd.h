@@ -383,8 +383,10 @@ int lsk_dispatch_timing_end(float* durations_us, int capacity, int* dispatches);
  * before the first multiply of segment s + 1 every workgroup waits until all
  * have finished segment s, on one arrival word per segment; mode 2: the same
  * on a two-level barrier (8 group words, the last arrival of each group
- * counts globally and releases its group).  The weight loads run ahead
- * across the waits.  workspace: lsk_probe_workspace_bytes() bytes,
+ * counts globally and releases its group); mode 3: the same on tag words
+ * (every workgroup stores s + 1 into its word of 8 replicas of a tag array
+ * and polls its replica until every word has reached it; at most 256 CUs).
+ * The weight loads run ahead across the waits.  workspace: lsk_probe_workspace_bytes() bytes,
  * zero-filled before first use; every launch leaves it zero except word 0,
  * which is nonzero after a bounded wait gave up.  No counterpart in the
  * reference. */

@@ -477,13 +477,16 @@ int lsk_probe_stream_step(const void* weights, size_t weight_bytes, const long l
   if (weights == nullptr || !aligned(weights, 16)) return fail(LSK_ERR_INVALID, "weights must be 16-byte aligned");
   if (seg_tiles == nullptr || count < 1 || count > lsk::kProbeMaxSegments)
     return fail(LSK_ERR_INVALID, "count=%d segments must be in 1..%d", count, lsk::kProbeMaxSegments);
-  if (mode < 0 || mode > 2) return fail(LSK_ERR_INVALID, "mode=%d must be 0, 1 or 2", mode);
+  if (mode < 0 || mode > 3) return fail(LSK_ERR_INVALID, "mode=%d must be 0, 1, 2 or 3", mode);
   if (ring != 4 && ring != 16) return fail(LSK_ERR_INVALID, "ring=%d must be 4 or 16", ring);
   if (workspace == nullptr || ws_bytes < lsk::kProbeWsBytes || !aligned(workspace, 4))
     return fail(LSK_ERR_WORKSPACE, "probe workspace needs %zu bytes (got %zu)", lsk::kProbeWsBytes, ws_bytes);
   int cus = 0;
   hipError_t err = lsk::current_device_cus(&cus);
   if (err != hipSuccess) return hip_fail(err, "device CU count");
+  if (mode == 3 && cus > lsk::kProbeMaxTagGroups)
+    return fail(LSK_ERR_INVALID, "mode 3 holds tag words for at most %d CUs (the device has %d)",
+                lsk::kProbeMaxTagGroups, cus);
   lsk::ProbeSegments seg{};
   seg.count = count;
   unsigned long long total = 0;

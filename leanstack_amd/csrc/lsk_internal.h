@@ -208,7 +208,8 @@ struct ProbeSegments {
 };
 // Workspace words: error, exit counter, checksum sink, the global arrival
 // word, 8 group words (16 apart), one flat arrival word per segment, 8 go
-// words per segment.
+// words per segment, then 8 replicas of one tag word per workgroup (mode 3,
+// at most kProbeMaxTagGroups workgroups).
 constexpr int kProbeWsError = 0;
 constexpr int kProbeWsExit = 1;
 constexpr int kProbeWsSink = 2;
@@ -216,7 +217,9 @@ constexpr int kProbeWsGlobal = 16;
 constexpr int kProbeWsGroups = 64;
 constexpr int kProbeWsFlat = 256;
 constexpr int kProbeWsGo = kProbeWsFlat + kProbeMaxSegments;
-constexpr size_t kProbeWsBytes = (size_t)(kProbeWsGo + 8 * kProbeMaxSegments) * 4;
+constexpr int kProbeMaxTagGroups = 256;
+constexpr int kProbeWsTags = kProbeWsGo + 8 * kProbeMaxSegments;
+constexpr size_t kProbeWsBytes = (size_t)(kProbeWsTags + 8 * kProbeMaxTagGroups) * 4;
 hipError_t launch_probe_step(const void* weights, const ProbeSegments& seg, int mode, int ring, int grid,
                              void* workspace, hipStream_t stream);
 hipError_t launch_probe_mfma(int workgroups, int iterations, void* sink, hipStream_t stream);

@@ -15,7 +15,11 @@
 //           per segment and polls it until all have arrived;
 //   mode 2  a two-level barrier: arrivals on 8 group words, the last arrival
 //           of each group counts on one global word, polls it and releases
-//           its group through a go word that the group polls.
+//           its group through a go word that the group polls;
+//   mode 3  tag words: every workgroup stores segment + 1 into its own word
+//           of 8 replicas of a tag array and polls the whole array of its
+//           replica (workgroup & 7) until every word has reached it: one
+//           store and one load round trip per boundary, no atomics.
 // Compute waves wait (in LDS) for the control wave before multiplying the
 // first tile of a segment, but their ring of weight loads runs ahead across
 // the wait.  Nothing is stored but a checksum; every wait is bounded.
@@ -60,6 +64,17 @@ __device__ __forceinline__ unsigned lds_load(unsigned* p) {
 }
 __device__ __forceinline__ void lds_store(unsigned* p, unsigned v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The least of words t[0..n) (n <= 256, agent scope, 4 per lane), uniform.
+__device__ __forceinline__ unsigned min_words(const unsigned* t, int n, int lane) {
+  unsigned m = 0xffffffffu;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (lane + 64 * i < n) m = min(m, ld_agent(t + lane + 64 * i));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = min(m, (unsigned)__shfl_xor((int)m, o));
+  return (unsigned)__builtin_amdgcn_readfirstlane((int)m);
 }
 
 // Waits until *p >= target (agent scope), or gives up: the error word is set
@@ -159,6 +174,19 @@ __global__ __launch_bounds__((kW + 1) * 64, 1) void probe_step_kernel(const char
       if (MODE == 1) {
         if (lane == 0) add_agent(flat + s, 1u);
         wait_at_least(flat + s, (unsigned)G, error);
+      } else if (MODE == 3) {
+        unsigned* tags = ws + kProbeWsTags;
+        if (lane < 8) st_agent(tags + lane * kProbeMaxTagGroups + c, (unsigned)s + 1);
+        const unsigned* mine = tags + grp * kProbeMaxTagGroups;
+        unsigned spins = 0;
+        while (min_words(mine, G, lane) < (unsigned)s + 1) {
+          if (ld_agent(error) != 0u) break;
+          __builtin_amdgcn_s_sleep(1);
+          if (++spins > kSpin) {
+            if (lane == 0) st_agent(error, 1u);
+            break;
+          }
+        }
       } else {
         unsigned old = 0;
         if (lane == 0) old = add_agent(group + grp * 16, 1u);
@@ -175,10 +203,16 @@ __global__ __launch_bounds__((kW + 1) * 64, 1) void probe_step_kernel(const char
       lds_store(&ready, (unsigned)s + 1);
     }
   }
-  // The last workgroup out clears the barrier words for the next launch.
+  // The last workgroup out clears the barrier and tag words for the next
+  // launch (every other workgroup has passed its last wait).
+  __shared__ unsigned last;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    if (add_agent(ws + kProbeWsExit, 1u) == (unsigned)G - 1) {
+  if (threadIdx.x == 0) last = add_agent(ws + kProbeWsExit, 1u) == (unsigned)G - 1 ? 1u : 0u;
+  __syncthreads();
+  if (last) {
+    if (MODE == 3)
+      for (int i = threadIdx.x; i < 8 * kProbeMaxTagGroups; i += blockDim.x) st_agent(ws + kProbeWsTags + i, 0u);
+    if (threadIdx.x == 0) {
       for (int i = 0; i < S; ++i) st_agent(ws + kProbeWsFlat + i, 0u);
       for (int i = 0; i < 8; ++i) st_agent(ws + kProbeWsGroups + i * 16, 0u);
       st_agent(ws + kProbeWsGlobal, 0u);
@@ -259,11 +293,13 @@ hipError_t launch_probe_step(const void* weights, const ProbeSegments& seg, int 
   if (ring == 4) {
     if (mode == 0) return go(probe_step_kernel<4, 0>);
     if (mode == 1) return go(probe_step_kernel<4, 1>);
-    return go(probe_step_kernel<4, 2>);
+    if (mode == 2) return go(probe_step_kernel<4, 2>);
+    return go(probe_step_kernel<4, 3>);
   }
   if (mode == 0) return go(probe_step_kernel<16, 0>);
   if (mode == 1) return go(probe_step_kernel<16, 1>);
-  return go(probe_step_kernel<16, 2>);
+  if (mode == 2) return go(probe_step_kernel<16, 2>);
+  return go(probe_step_kernel<16, 3>);
 }
 
 }  // namespace lsk

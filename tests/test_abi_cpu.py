@@ -339,7 +339,8 @@ def test_probe_rejects_before_launch():
 
     assert call(count=0) == _lib.ERR_INVALID
     assert call(count=257) == _lib.ERR_INVALID
-    assert call(mode=3) == _lib.ERR_INVALID
+    assert call(mode=4) == _lib.ERR_INVALID
+    assert call(mode=-1) == _lib.ERR_INVALID
     assert call(ring=8) == _lib.ERR_INVALID
     assert call(weights=fake + 8) == _lib.ERR_INVALID
     assert call(ws_bytes=need - 4) == _lib.ERR_WORKSPACE

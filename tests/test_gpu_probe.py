@@ -14,7 +14,7 @@ from leanstack_amd import _lib
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
 @pytest.mark.parametrize("ring", [4, 16])
 def test_probe_modes_complete(gpu, mode, ring):
     lib = _lib.load()
