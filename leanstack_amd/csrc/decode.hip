@@ -617,10 +617,7 @@ __device__ __forceinline__ unsigned long long load_partial(const ArgmaxPartial* 
 }
 
 constexpr unsigned kHeadSpinLimit = 1u << 20;  // polls of one partial before the second stage gives up
-#ifndef LSK_LMHEAD_ROUND
-#define LSK_LMHEAD_ROUND 10
-#endif
-constexpr int kRoundLoads = LSK_LMHEAD_ROUND;                 // partial loads in flight per thread of the second stage
+constexpr int kRoundLoads = 10;  // partial loads in flight per thread of the second stage
 
 // Second stage of the greedy head, as the host-side torch.argmax over tile
 // maxima in src/leanstack/runtime/cutile_logits.py:67-69: the NT threads of
@@ -800,10 +797,7 @@ __global__ __launch_bounds__(NW * 64) void lm_head_kernel(
 }
 
 constexpr int kLmHeadWaves = 8;
-#ifndef LSK_LMHEAD_RBW
-#define LSK_LMHEAD_RBW 2
-#endif
-constexpr int kLmHeadRBW = LSK_LMHEAD_RBW;
+constexpr int kLmHeadRBW = 2;
 
 // Launch arguments of one decode / verify projection.
 struct DecodeArgs {
@@ -1143,10 +1137,7 @@ hipError_t launch_lm_head_argmax(const void* w, int V, int K, const void* x, int
   // K/32 = 80: 8 waves x 10 k-tiles; for M <= 8 the activations are staged
   // through LDS (the wave's 40 M chunks over 64 lanes).
   if (KT == 80 && M <= 8) {
-#ifndef LSK_LMHEAD_NC_MIN
-#define LSK_LMHEAD_NC_MIN 1
-#endif
-    switch (std::max((40 * M + 63) / 64, LSK_LMHEAD_NC_MIN)) {
+    switch ((40 * M + 63) / 64) {
       case 1:
         staged(std::integral_constant<int, 1>{});
         break;

@@ -32,12 +32,9 @@ constexpr int kMaxActivationStride = (1 << 22) - 8;
 // 8 * kAttnSplitRows rows as at most 8 chunks of kAttnSplitRows rows (one
 // combine round); beyond that, at most kAttnMaxChunks chunks of the smallest
 // multiple of kAttnMinChunkRows rows that allows it.
-#ifndef LSK_ATTN_SPLIT_ROWS
-#define LSK_ATTN_SPLIT_ROWS 64
-#endif
 constexpr int kAttnHeadDim = 128;
 constexpr int kAttnMinChunkRows = 128;
-constexpr int kAttnSplitRows = LSK_ATTN_SPLIT_ROWS;
+constexpr int kAttnSplitRows = 64;
 constexpr int kAttnMaxChunkRows = 512;
 constexpr int kAttnMaxChunks = 32;
 constexpr int kAttnMaxRows = kAttnMaxChunks * kAttnMaxChunkRows;  // 16384

@@ -59,10 +59,7 @@ constexpr int kCompute = kStackComputeWaves;          // 8
 constexpr int kThreads = (kCompute + 2) * 64;         // + stager and finisher waves
 constexpr int kSeg = kStackSegTiles;                  // 16 k-tiles (512 K) per segment
 constexpr int kWaveTiles = kSeg / kCompute;           // 2 k-tiles per compute wave per segment
-#ifndef LSK_RING
-#define LSK_RING 16
-#endif
-constexpr int kRing = LSK_RING;                             // weight tiles in flight per compute wave
+constexpr int kRing = 16;                             // weight tiles in flight per compute wave
 constexpr int kXRow = kSeg * kTileK * 2 + 16;         // LDS bytes per activation row (+16: bank skew)
 constexpr int kXBytes = 104 * 1024;                   // staged activation segments (M rows each)
 constexpr int kMaxXSlots = 64;
