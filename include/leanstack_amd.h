@@ -229,7 +229,9 @@ int lsk_decode_attention_at_bf16(const void* qkv, int n_q, int n_kv, int head_di
                                  void* hip_stream);
 
 /* Greedy lm_head: out_idx[m] = argmax_v sum_k f32(W[v][k]) * f32(x[m][k]) for
- * m < M (M = 1..16), lowest index on ties.
+ * m < M (M = 1..16), lowest index on ties.  V % 16 == 0 (whole packed
+ * row-blocks; a tensor-parallel vocab shard, e.g. 151936 / 8 = 18992, has an
+ * odd count of them), K % 32 == 0.
  *   logits_mode  LSK_LOGITS_FP32 compares fp32 scores, as the cuTile kernel
  *                does (src/leanstack/runtime/cutile_logits.py:17-31, :67-69);
  *                LSK_LOGITS_BF16 compares bf16-rounded logits, as
@@ -275,10 +277,10 @@ int lsk_rmsnorm_lm_head_argmax_bf16(const void* w_packed, int layout_id, int V, 
  * time), so the call allocates nothing.  No counterpart in the reference; it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Limit:
- * 64 + M * P * 8 bytes, P = (V/16 - 512) / 2 + 512 (the scoring
- * workgroups), must fit in 1 MiB (every M <= 16 at
- * V = 151936); larger calls return LSK_ERR_INVALID before anything touches
- * the GPU.  All calls on one
+ * 64 + M * P * 8 bytes must fit in 1 MiB, P the scoring workgroups: with
+ * NB = V/16 row-blocks, P = NB up to 512 of them, else (NB - T)/2 + T with
+ * T = 512 + (NB - 512) % 2 (every M <= 16 at V = 151936, P = 5004); larger
+ * calls return LSK_ERR_INVALID before anything touches the GPU.  All calls on one
  * device share the array: calls that overlap in time on a device (streams not
  * ordered with each other) race; stream-ordered calls do not. */
 int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_id, int V, int K,

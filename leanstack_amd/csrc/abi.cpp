@@ -109,7 +109,7 @@ size_t lsk_workspace_bytes(int op, int M, int N, int K) {
     return err == hipSuccess ? bytes : 0;
   }
   if (op == LSK_OP_LM_HEAD_ARGMAX) {
-    if (M < 1 || M > lsk::kDecodeMaxM || N <= 0 || K <= 0 || N % (2 * lsk::kTileRows) != 0) return 0;
+    if (M < 1 || M > lsk::kDecodeMaxM || N <= 0 || K <= 0 || N % lsk::kTileRows != 0) return 0;
     return lsk::lm_head_workspace_bytes(M, N);
   }
   return 0;

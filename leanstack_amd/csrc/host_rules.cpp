@@ -124,9 +124,7 @@ int check_lm_head(const void* w_packed, int layout_id, int V, int K, const void*
                   const float* logits_opt, int logits_mode, const long long* out_idx) {
   if (layout_id != LSK_LAYOUT_MFMA16X32)
     return fail(LSK_ERR_LAYOUT, "lm_head needs layout %d, got %d", LSK_LAYOUT_MFMA16X32, layout_id);
-  if (int st = check_shape(layout_id, V, K)) return st;
-  if (V % (2 * kTileRows) != 0)
-    return fail(LSK_ERR_INVALID, "vocab size V=%d must be divisible by %d", V, 2 * kTileRows);
+  if (int st = check_shape(layout_id, V, K)) return st;  // V % 16 == 0: whole row-blocks, any count
   if (M < 1 || M > kDecodeMaxM) return fail(LSK_ERR_INVALID, "M=%d must be in 1..%d", M, kDecodeMaxM);
   if (logits_mode != LSK_LOGITS_FP32 && logits_mode != LSK_LOGITS_BF16)
     return fail(LSK_ERR_INVALID, "unknown logits mode %d", logits_mode);

@@ -163,7 +163,10 @@ hipError_t launch_decode_attention_at(const void* qkv, int n_q, int n_kv, const 
                                       void* v_cache, int s_max, const int* pos_device, float scale, void* out,
                                       void* workspace, size_t ws_bytes, hipStream_t stream);
 
-// Number of workgroups (= argmax partials per row) the lm_head kernel uses.
+// Number of scoring workgroups (= argmax partials per row) the lm_head
+// kernel uses for V vocab rows (V % 16 == 0): with NB = V / 16 row-blocks,
+// NB if NB <= 512, else (NB - T) / 2 + T with T = 512 + (NB - 512) % 2 (pairs
+// of row-blocks, then T single ones).
 int lm_head_partials(int V);
 
 // The lm_head workspace: a status header (word 0 counts second stages that

@@ -62,7 +62,7 @@ extern "C" int lsk_lm_head_argmax_noalloc_bf16(const void* w_packed, int layout_
   if (need > kScratchBytes) {
     return lsk::fail(LSK_ERR_INVALID,
                      "M=%d rows over V=%d need %zu bytes of argmax workspace; the static scratch holds %zu "
-                     "(64 + M * P * 8 bytes, P = (V/16 - 512) / 2 + 512): use lsk_lm_head_argmax_bf16 with a workspace",
+                     "(64 + M * P * 8 bytes, P the scoring workgroups): use lsk_lm_head_argmax_bf16 with a workspace",
                      M, V, need, kScratchBytes);
   }
   int device = 0;

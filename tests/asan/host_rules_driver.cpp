@@ -85,7 +85,8 @@ int main() {
   expect(lsk::check_lm_head(p, 1, 151936, 2560, p, 8, 2560, nullptr, 0, idx) == LSK_OK, "valid lm_head");
   expect(lsk::check_lm_head(p, 2, 151936, 2560, p, 8, 2560, nullptr, 0, idx) == LSK_ERR_LAYOUT, "lm_head layout");
   expect(lsk::check_lm_head(p, 1, 151936, 2560, p, 17, 2560, nullptr, 0, idx) == LSK_ERR_INVALID, "lm_head M = 17");
-  expect(lsk::check_lm_head(p, 1, 151920, 2560, p, 1, 2560, nullptr, 0, idx) == LSK_ERR_INVALID, "V % 32");
+  expect(lsk::check_lm_head(p, 1, 151928, 2560, p, 1, 2560, nullptr, 0, idx) == LSK_ERR_INVALID, "V % 16");
+  expect(lsk::check_lm_head(p, 1, 18992, 2560, p, 1, 2560, nullptr, 0, idx) == LSK_OK, "odd count of row-blocks");
 
   if (g_failures) {
     std::printf("%d checks failed\n", g_failures);

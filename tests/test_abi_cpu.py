@@ -165,9 +165,15 @@ def test_lm_head_rejects_before_launch():
     # status header + one partial per scoring workgroup: 4492 of two 16-row
     # vocab blocks, then a tail of 512 single blocks (151936 / 16 = 9496 = 2 * 4492 + 512)
     assert ws == 64 + (4492 + 512) * 8
+    # an odd count of row-blocks (the vocab shard of 8-way tensor parallelism,
+    # 151936 / 8 = 18992 = 16 * 1187): 337 pairs, then a tail of 513 single blocks
+    assert lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 1, 18992, 2560) == 64 + (337 + 513) * 8
+    # up to 512 row-blocks, one workgroup each
+    assert lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 2, 16 * 101, 2560) == 64 + 2 * 101 * 8
+    assert lib.lsk_workspace_bytes(_lib.OP_LM_HEAD_ARGMAX, 1, 151928, 2560) == 0  # V % 16 != 0
     cases = [
         (dict(M=17), _lib.ERR_INVALID),
-        (dict(V=151920), _lib.ERR_INVALID),   # V % 32 != 0
+        (dict(V=151928), _lib.ERR_INVALID),   # V % 16 != 0: not whole row-blocks
         (dict(mode=3), _lib.ERR_INVALID),
         (dict(ws=ws - 8), _lib.ERR_WORKSPACE),
         (dict(layout=2), _lib.ERR_LAYOUT),
@@ -290,8 +296,8 @@ def test_launch_next_refuses_a_bad_token_buffer():
 
 def test_noalloc_lm_head_rejects_before_launch():
     """The allocation-free head refuses calls whose workspace exceeds its
-    static scratch (64 + M * P * 8 bytes > 1 MiB, P = (V/16 - 512) / 2 + 512
-    scoring workgroups) and the usual bad arguments, before touching the GPU."""
+    static scratch (64 + M * P * 8 bytes > 1 MiB, P the scoring workgroups)
+    and the usual bad arguments, before touching the GPU."""
     lib = _lib.load()
 
     def call(**over):

@@ -407,13 +407,15 @@ def test_lm_head_ties_pick_lowest_index(gpu):
         assert idx.tolist() == [1234]
 
 
-@pytest.mark.parametrize("v", [16 * 512, 16 * 514, 16 * 2048])
+@pytest.mark.parametrize("v", [16 * 101, 16 * 512, 16 * 513, 16 * 514, 16 * 1187, 16 * 2048])
 def test_lm_head_tail_workgroups(gpu, v):
     """The scoring grid takes two 16-row vocab blocks per workgroup, then a
-    tail of 512 one-block workgroups (all one-block up to 512 blocks): at
-    512, 514 and 2048 blocks every row's fp32 score equals the CPU's (each
-    row scored once, in its own place), and a maximum planted in the first
-    and last pair, the first and last tail block and the last row is found."""
+    tail of 512 one-block workgroups (513 when the count past 512 is odd; all
+    one-block up to 512 blocks): at 101, 512, 513, 514, 1187 (the vocab shard
+    of 8-way tensor parallelism) and 2048 blocks every row's fp32 score equals
+    the CPU's (each row scored once, in its own place), and a maximum planted
+    in the first and last pair, the first and last tail block and the last
+    row is found."""
     k = 256
     dev = torch.device("cuda:0")
     h = activations(1, k, seed=740)
