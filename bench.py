@@ -15,8 +15,10 @@ gate_up kernels, or as separate F.rms_norm launches), a whole decode token with
 attention over 320 and 4095 cached rows (every layer HIP), a greedy decode loop in
 the reference's decode_64_256 shape (256 tokens after 64 cached rows, one graph
 replay per token, per-step events), each projection kind's
-per-launch time, the tied lm_head + argmax at M = 1..8, and the prefill GEMMs
-at M = 512, 2048, 8192 in TFLOP/s.
+per-launch time, the tied lm_head + argmax at M = 1..8, the prefill GEMMs
+at M = 512, 2048, 8192 in TFLOP/s, and one GPU's share of 8-way tensor
+parallelism at the real shard shapes (its M = 1 step, lm_head and prefill
+layer; the all-reduces between shards are not run).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -30,6 +32,7 @@ import platform
 import statistics
 import sys
 import time
+import types
 from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
@@ -235,6 +238,110 @@ def prefill_graph_times(torch, kernels, lib, stack, layer, m: int, steps: int, g
     return out
 
 
+TP_DEGREE = 8
+
+
+def tp_shard(torch, kernels, lib, stack, g, steps: int, warmup: int, gen, dev, prefill_tokens: int | None) -> dict:
+    """One GPU's share of TP_DEGREE-way tensor parallelism at the real shard
+    shapes: QKV split by output rows (4 q heads + 1 kv head, 768 x 2560),
+    o_proj by its K (2560 x 512), gate_up by output rows keeping the gate/up
+    pairing (2 x 1216 x 2560, SiLU*up), down by its K (2560 x 1216), the tied
+    lm_head by vocab (18992 x 2560).  Timed: the shard's 36-layer M = 1 step
+    (144 launches in one graph over 36 distinct shard layers), each shard
+    projection over 36 launches, the shard's greedy head (4 calls per
+    replay), and its prefill layer at `prefill_tokens` tokens (None: not
+    timed).  The all-reduces that would join the shards are not run."""
+    from leanstack_amd.layout import PackedWeight
+
+    tp, h, inter, n_l = TP_DEGREE, g.hidden_size, g.intermediate_size, g.num_hidden_layers
+    shapes = {"qkv_proj": (g.qkv_dim // tp, h), "o_proj": (h, g.q_dim // tp),
+              "gate_up_proj": (2 * inter // tp, h), "down_proj": (h, inter // tp)}
+
+    def pack(name):
+        n, k = shapes[name]
+        w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        return PackedWeight.from_rowmajor(
+            w, lib.LAYOUT_MFMA16X32_GATEUP if name == "gate_up_proj" else lib.LAYOUT_MFMA16X32)
+
+    def call_bytes(name, m):
+        n, k = shapes[name]
+        return n * k * 2 + m * k * 2 + m * (n // 2 if name == "gate_up_proj" else n) * 2
+
+    layers = [{name: pack(name) for name in shapes} for _ in range(n_l)]
+    x = {name: torch.randn((n_l, 1, shapes[name][1]), generator=gen, device=dev).to(torch.bfloat16)
+         for name in ("qkv_proj", "o_proj", "gate_up_proj")}
+    y = {"qkv_proj": torch.empty((1, shapes["qkv_proj"][0]), device=dev, dtype=torch.bfloat16),
+         "o_proj": torch.empty((1, h), device=dev, dtype=torch.bfloat16),
+         "gate_up_proj": torch.empty((1, inter // tp), device=dev, dtype=torch.bfloat16),
+         "down_proj": torch.empty((1, h), device=dev, dtype=torch.bfloat16)}
+
+    def launch(name, l):
+        if name == "down_proj":  # reads the activation gate_up wrote, as in the full step
+            kernels.linear(y["gate_up_proj"], layers[l][name], out=y[name])
+        else:
+            epi = lib.EPI_SILU_MUL if name == "gate_up_proj" else lib.EPI_NONE
+            kernels.linear(x[name][l], layers[l][name], epilogue=epi, out=y[name])
+
+    graph = stack.capture(lambda: [launch(name, l) for l in range(n_l) for name in shapes])
+    settle(torch, graph, 0.1)
+    ms = time_graph(torch, graph, steps, warmup)
+    del graph
+    step_bytes = n_l * sum(call_bytes(name, 1) for name in shapes)
+    res = {
+        "tp": tp,
+        "shapes": {name: list(s) for name, s in shapes.items()},
+        "decode_step_m1": {"us": round(ms * 1e3, 1), "launches": 4 * n_l, "bytes": step_bytes,
+                           "GB/s": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+                           "frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                           "floor_us_at_hbm_peak": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e6, 1)},
+        "per_projection_m1": {},
+        "not_run": "the two all-reduces of [M, 2560] per layer and the head's (max, index) exchange (one GPU)",
+    }
+    log(f"tp{tp} shard step M=1: {ms * 1e3:.1f} us ({res['decode_step_m1']['GB/s']} GB/s, floor "
+        f"{res['decode_step_m1']['floor_us_at_hbm_peak']} us)")
+    for name in shapes:
+        graph = stack.capture(lambda name=name: [launch(name, l) for l in range(n_l)])
+        us = time_graph(torch, graph, steps, warmup) * 1e3 / n_l
+        del graph
+        res["per_projection_m1"][name] = {"us_per_launch": round(us, 2),
+                                          "GB/s": round(call_bytes(name, 1) / (us * 1e-6) / 1e9, 1)}
+        log(f"tp{tp} shard {name} {shapes[name][0]}x{shapes[name][1]} M=1: {us:.2f} us/launch")
+    del layers, x, y
+
+    v = g.vocab_size // tp
+    e = PackedWeight.from_rowmajor((torch.randn((v, h), generator=gen, device=dev) * 0.02).to(torch.bfloat16))
+    hidden = torch.randn((1, h), generator=gen, device=dev).to(torch.bfloat16)
+    ws = kernels.LmHeadWorkspace(1, v, h, dev)
+    tok = torch.empty((1,), device=dev, dtype=torch.long)
+    reps = 4
+    graph = stack.capture(lambda: [kernels.lm_head_argmax(hidden, e, workspace=ws, out=tok) for _ in range(reps)])
+    us = time_graph(torch, graph, steps, warmup) * 1e3 / reps
+    del graph
+    head_bytes = v * h * 2 + h * 2
+    res["lm_head_m1"] = {"vocab_rows": v, "us": round(us, 2), "GB/s": round(head_bytes / (us * 1e-6) / 1e9, 1)}
+    log(f"tp{tp} shard lm_head {v}x{h} M=1: {us:.2f} us")
+    del e
+
+    if prefill_tokens is not None:
+        m = prefill_tokens
+        p0 = {name: pack(name) for name in shapes}
+        layer = types.SimpleNamespace(qkv=p0["qkv_proj"], o=p0["o_proj"], gate_up=p0["gate_up_proj"],
+                                      down=p0["down_proj"])
+        times = prefill_graph_times(torch, kernels, lib, stack, layer, m, steps, gen, dev)
+        flops = {name: 2 * m * shapes[name][0] * shapes[name][1] for name in shapes}
+        layer_us = sum(times.values())
+        res["prefill"] = {
+            "tokens": m,
+            "layer_us": round(layer_us, 1),
+            "layer_TFLOP/s": round(sum(flops.values()) / (layer_us * 1e-6) / 1e12, 1),
+            "per_projection": {name: {"us": round(us, 1), "TFLOP/s": round(flops[name] / (us * 1e-6) / 1e12, 1)}
+                               for name, us in times.items()},
+        }
+        log(f"tp{tp} shard prefill M={m}: layer {res['prefill']['layer_us']} us, "
+            f"{res['prefill']['layer_TFLOP/s']} TFLOP/s")
+    return res
+
+
 def step_kernel_durations(kernels, stack, g, reps: int) -> dict[str, list[float]]:
     """Each dispatch's own duration (us) over `reps` eager launches of the
     36-layer M = 1 step, by projection (the step launches qkv, o, gate_up,
@@ -422,6 +529,9 @@ def main() -> int:
     ap.add_argument("--probe-mfma", action="store_true",
                     help="only the MFMA-rate probe (lsk_probe_mfma_rate): dense BF16 MFMAs with no memory traffic, "
                          "on every CU and on 32")
+    ap.add_argument("--tp-shard-only", action="store_true",
+                    help="only the tensor-parallel shard measurements (one GPU's share of 8-way TP at the real "
+                         "shard shapes: the 36-layer M = 1 step, the lm_head, the prefill layer at 2048 tokens)")
     ap.add_argument("--pmc-prefill", action="store_true",
                     help="short run for hardware-counter profiling of the prefill GEMMs: each projection at "
                          "M = 512, 2048 and 8192, three launches each, no graphs")
@@ -519,6 +629,11 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"pmc_run": True, "copy_bytes": 2 * src.numel(),
                           "bytes_per_launch": {n: G.projection_bytes(n, 1) for n in G.projections()}}), flush=True)
+        return 0
+
+    if args.tp_shard_only:
+        shard = tp_shard(torch, kernels, _lib, stack, G, steps, warmup, gen, dev, 2048)
+        print(json.dumps({"tp_shard": shard}), flush=True)
         return 0
 
     if args.pmc_prefill:
@@ -765,6 +880,9 @@ def main() -> int:
             "mfma_util_source": "profiles/prefill_gemm_counters.md (rocprofv3 --pmc MfmaUtil, bench.py --pmc-prefill)",
         }
 
+    # --- one GPU's share of 8-way tensor parallelism ---------------------------
+    shard = tp_shard(torch, kernels, _lib, stack, G, steps, warmup, gen, dev, None if args.quick else 2048)
+
     cpu = None
     if not args.quick:
         cpu = cpu_baseline(G, args.cpu_seconds)
@@ -828,6 +946,7 @@ def main() -> int:
             "lm_head_argmax": {str(m): v for m, v in head.items()},
             "prefill": {str(m): v for m, v in prefill.items()},
             "hot_kernel_cases": hot,
+            "tp8_shard": shard,
             "device": torch.cuda.get_device_name(0),
         },
     }
