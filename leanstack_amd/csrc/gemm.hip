@@ -4,7 +4,7 @@
 // kernels; launch_gemm_linear at the end of this file picks one:
 //
 //  * wdx::gemm_wdx_kernel, the prefill GEMM proper (M > 128, N a multiple of
-//    256 or 192, K of 128: every Qwen3-4B projection).  256 tokens x 256, 192
+//    128 or 192, K of 128: every Qwen3-4B projection).  256 tokens x 256, 192
 //    or 128 weight rows x 64 K per stage and workgroup on
 //    v_mfma_f32_32x32x16_bf16: weight fragments from HBM/L2 straight into
 //    registers one stage ahead, activations DMA'd into a three-buffer LDS ring
@@ -15,7 +15,8 @@
 //    for the M > 128 shapes with N a multiple of 256 that the wdx kernel does
 //    not take (K an odd multiple of 64).
 //  * gemm_linear_kernel, 128 x 128 blocks for the rest of the 128-row grid
-//    (M = 17..128, or N a multiple of 128 only).  Each packed 1 KB weight
+//    (65..128 rows of N >= 8192, or N a multiple of 128 with K an odd
+//    multiple of 64 that the 256 x 256 kernel cannot take).  Each packed 1 KB weight
 //    tile already is a v_mfma_f32_16x16x32_bf16 operand in lane order, so the
 //    weight half of every LDS stage is a straight linear copy; the activation
 //    half is re-tiled into the same operand order as it is copied, so both
@@ -1165,8 +1166,11 @@ inline void split_plan(int T, int units, int grid, int* R, int* S) {
 // rows), and a split round adds about 0.06 us per block row for its partial
 // exchange.  QKV at 768 and 1024 tokens 37.2 -> 32.6 and 41.1 -> 36.3 us,
 // o_proj at 3072 66.1 -> 61.8; down_proj at 3072 (152 stages) keeps its
-// split 256-row round.
+// split 256-row round.  And 1 whenever N is a multiple of 128 but of neither
+// 192 nor 256 (e.g. the gate_up shard of 8-way tensor parallelism, 2432
+// rows), which the 128 x 128 kernel would otherwise take.
 inline int choose_tiles(int N, int m_blocks, int grid, int units, int split_grid) {
+  if (N % kRowsWide != 0 && N % kRows192 != 0) return 1;  // N on the 128-row grid only
   int a = 4;
   if (N % kRows192 != 0) {
     a = 4;
@@ -1230,7 +1234,7 @@ hipError_t launch_cfg(const void* w, int N, int K, const void* x, int M, int ldx
 namespace {
 
 bool sk_shape(int M, int N, int K) {
-  return M > kGemmBM && (N % wdx::kRowsWide == 0 || N % wdx::kRows192 == 0) && K % (2 * wdx::BK) == 0;
+  return M > kGemmBM && (N % wdx::kRows128 == 0 || N % wdx::kRows192 == 0) && K % (2 * wdx::BK) == 0;
 }
 
 // Workgroups resident at once on `device` (the kernel holds 512 registers
